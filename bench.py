@@ -1,0 +1,277 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized paged decode attention hot path on one MI355X.
+
+Workload (the metric's config): Llama-3-8B-shaped
+single-layer decode — 32 query / 8 KV heads (GQA 4), head_dim 128, batch 16,
+every sequence at 32,768 tokens = 32 FP16 sinks + 255 INT2/INT4 pages of 128
+tokens + 96 FP16 tail tokens; 12.5% of key channels INT4 (16 outlier channels
+per head scaled x8, chosen by 256 seeded calibration tokens).  K/V are fp16
+N(0,1), quantised into the pools by the HIP quantize kernel; pages are placed
+through a shuffled free list.  Three independent pool copies (~953 MB) rotate
+step to step so no step is served from the 256 MB MALL.
+
+One step = one decode layer-step: the split-K kernel plus the merge kernel for
+all 16 sequences.  `value` is microseconds per layer-step (wall clock over the
+timed steps, inputs resident in HBM); the roofline entry is for the dominant
+kernel (split-K decode), timed with HIP events on the stream it runs on.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "kitty-kv_amd"))
+
+HBM_PEAK_GBPS = 8000.0
+
+CONFIGS = {
+    "cfg3": dict(B=16, Hq=32, Hkv=8, ctx=32768, boost=0.125, outlier=8.0, seed=3),
+    "cfg5": dict(B=4, Hq=64, Hkv=8, ctx=131072, boost=0.125, outlier=16.0, seed=5),
+}
+D, G, S = 128, 128, 32
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_workload(torch, dev, cfg, copies: int):
+    from kitty.kernels.ops import DecodePlan, pool_store, quantize_into_pools
+    B, Hq, Hkv, ctx = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["ctx"]
+    dk = round(cfg["boost"] * D)
+    sentinel = min(dk + 1, 255)
+    n_pages = (ctx - S) // G
+    n_tail = (ctx - S) % G
+    gen = torch.Generator(device="cpu").manual_seed(cfg["seed"])
+    chans = torch.stack([torch.randperm(D, generator=gen)[:dk] for _ in range(Hkv)])
+    calib = torch.randn(256, Hkv, D, generator=gen)
+    for h in range(Hkv):
+        calib[:, h, chans[h]] *= cfg["outlier"]
+    score = calib.abs().mean(0)
+    order = torch.argsort(score, dim=-1, descending=True, stable=True)
+    bi = torch.full((Hkv, D), sentinel, dtype=torch.uint8)
+    for r in range(dk):
+        bi[torch.arange(Hkv), order[:, r]] = r
+    bi = bi.to(dev)
+
+    used = copies * B * n_pages
+    P = used + 8
+    kb = torch.empty(P, Hkv, D, G // 4, dtype=torch.uint8, device=dev)
+    kh = torch.empty(P, Hkv, dk, G // 4, dtype=torch.uint8, device=dev)
+    km = torch.empty(P, Hkv, 2, D, dtype=torch.float16, device=dev)
+    vp = torch.empty(P, Hkv, G, D // 4, dtype=torch.uint8, device=dev)
+    vm = torch.empty(P, Hkv, G, 2, dtype=torch.float16, device=dev)
+    store = pool_store(kb, kh, km, vp, vm)
+    placement = torch.randperm(P, generator=gen)[:used].to(torch.int32)   # shuffled free list
+    g = torch.Generator(device=dev).manual_seed(cfg["seed"] + 100)
+    scale = torch.ones(Hkv, D, device=dev)
+    for h in range(Hkv):
+        scale[h, chans[h].to(dev)] = cfg["outlier"]
+    chunk = 1024
+    for p0 in range(0, used, chunk):
+        n = min(chunk, used - p0)
+        k = (torch.randn(n, Hkv, G, D, device=dev, generator=g) * scale[None, :, None, :]).half()
+        v = torch.randn(n, Hkv, G, D, device=dev, generator=g).half()
+        quantize_into_pools(store, k, v, bi, placement[p0:p0 + n].to(dev), sentinel)
+    torch.cuda.synchronize()
+
+    q = torch.randn(B, Hq, D, device=dev, generator=g).half()
+    sk = torch.randn(B, Hkv, S, D, device=dev, generator=g).half()
+    sv = torch.randn(B, Hkv, S, D, device=dev, generator=g).half()
+    tk = torch.randn(B, Hkv, max(n_tail, 1), D, device=dev, generator=g).half()
+    tv = torch.randn(B, Hkv, max(n_tail, 1), D, device=dev, generator=g).half()
+    npg = torch.full((B,), n_pages, dtype=torch.int32, device=dev)
+    sl = torch.full((B,), S, dtype=torch.int32, device=dev)
+    tl = torch.full((B,), n_tail, dtype=torch.int32, device=dev)
+    out = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
+    plans, tables = [], []
+    for c in range(copies):
+        bt = placement[c * B * n_pages:(c + 1) * B * n_pages].view(B, n_pages).contiguous().to(dev)
+        tables.append(bt)
+        plans.append(DecodePlan(q, bt, npg, kb, kh, km, vp, vm, bi, sk, sv, sl, tk, tv, tl, out=out))
+    w = dict(B=B, Hq=Hq, Hkv=Hkv, dk=dk, n_pages=n_pages, n_tail=n_tail, P=P, pools=(kb, kh, km, vp, vm),
+             tables=tables, q=q, sk=sk, sv=sv, tk=tk, tv=tv, bi=bi, plans=plans, out=out)
+    return w
+
+
+def algorithmic_bytes(w) -> dict:
+    B, Hkv, Hq, n_pages, dk = w["B"], w["Hkv"], w["Hq"], w["n_pages"], w["dk"]
+    per_page_head = D * G // 4 + dk * G // 4 + 2 * D * 2 + G * D // 4 + G * 2 * 2
+    packed = B * Hkv * n_pages * per_page_head
+    fp16 = B * Hkv * (S + w["n_tail"]) * D * 2 * 2
+    small = B * Hq * D * 2 + B * n_pages * 4 + Hkv * D + 3 * B * 4
+    return dict(per_page_head=per_page_head, packed=packed, fp16=fp16, total=packed + fp16 + small)
+
+
+def cpu_baseline(w, budget_s: float) -> dict:
+    """Oracle C port of paged_attention_reference, one thread, on whole
+    sequences of the same workload until ~budget_s of CPU work."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    O.build()
+    kb, kh, km, vp, vm = w["pools"]
+    bt = w["tables"][0]
+    n = w["n_tail"]
+    done, t_total = 0, 0.0
+    while done < w["B"] and (t_total < budget_s or done == 0):
+        b = done
+        idx = bt[b].long()
+        sub = [t[idx].cpu().numpy() for t in (kb, kh, km, vp, vm)]
+        args = (w["q"][b].cpu().numpy(), np.arange(w["n_pages"], dtype=np.int32), *sub, w["bi"].cpu().numpy(),
+                w["dk"], w["sk"][b].cpu().numpy(), w["sv"][b].cpu().numpy(), w["tk"][b, :, :n].cpu().numpy(),
+                w["tv"][b, :, :n].cpu().numpy(), w["Hq"], w["Hkv"], D)
+        t0 = time.perf_counter()
+        O.paged_attention(*args, n_threads=1)
+        t_total += time.perf_counter() - t0
+        done += 1
+    per_seq = t_total / done
+    return {"value": round(per_seq * w["B"] * 1e6, 1), "unit": "us/layer-step", "cores": 1, "kind": "port",
+            "sample": f"{done} of {w['B']} sequences (all {w['Hkv']} KV heads, {w['n_pages']} pages + "
+                      f"{S} sinks + {n} tail tokens each) through oracle/kitty_oracle.c "
+                      f"(paged_attention_reference restated), single thread; x{w['B']}/{done} to one layer-step"}
+
+
+def bench_quantize(torch, dev, reps: int = 20) -> dict:
+    """4096 tokens x 8 KV heads x 128, batch quantize + pack."""
+    from kitty.kernels.ops import pool_store, quantize_into_pools
+    T, H, dk = 4096, 8, 16
+    n = T // G
+    g = torch.Generator(device=dev).manual_seed(2)
+    pools = [torch.empty(n * 3, H, D, G // 4, dtype=torch.uint8, device=dev),
+             torch.empty(n * 3, H, dk, G // 4, dtype=torch.uint8, device=dev),
+             torch.empty(n * 3, H, 2, D, dtype=torch.float16, device=dev),
+             torch.empty(n * 3, H, G, D // 4, dtype=torch.uint8, device=dev),
+             torch.empty(n * 3, H, G, 2, dtype=torch.float16, device=dev)]
+    store = pool_store(*pools)
+    bi = torch.full((H, D), dk + 1, dtype=torch.uint8)
+    for h in range(H):
+        bi[h, torch.randperm(D)[:dk]] = torch.arange(dk, dtype=torch.uint8)
+    bi = bi.to(dev)
+    ks = [torch.randn(T, H, D, device=dev, generator=g).half() for _ in range(3)]
+    vs = [torch.randn(T, H, D, device=dev, generator=g).half() for _ in range(3)]
+    pids = [torch.arange(i * n, (i + 1) * n, dtype=torch.int32, device=dev) for i in range(3)]
+
+    def run(i):
+        kv = ks[i % 3].view(n, G, H, D).permute(0, 2, 1, 3)
+        vv = vs[i % 3].view(n, G, H, D).permute(0, 2, 1, 3)
+        quantize_into_pools(store, kv, vv, bi, pids[i % 3], dk + 1)
+
+    for i in range(5):
+        run(i)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for i in range(reps):
+        evs[i][0].record()
+        run(i)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    us = sum(a.elapsed_time(b) for a, b in evs) / reps * 1e3
+    read = 2 * T * H * D * 2
+    written = n * H * (D * G // 4 + dk * G // 4 + 2 * D * 2 + G * D // 4 + G * 2 * 2)
+    return {"workload": "cfg2: 4096 tok x 8 KV heads x 128, 12.5% INT4", "us": round(us, 2),
+            "GBps": round((read + written) / us / 1e3, 1), "bytes_read": read, "bytes_written": written}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="cfg3")
+    ap.add_argument("--copies", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-quantize", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every box has one MI355X); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    log(f"building {args.config} workload ({args.copies} pool copies)")
+    w = build_workload(torch, dev, cfg, args.copies)
+    nb = algorithmic_bytes(w)
+    plans = w["plans"]
+    log(f"pool {w['P']} pages, {nb['packed'] / 1e6:.1f} MB packed KV per step; warmup {args.warmup}")
+    for i in range(args.warmup):
+        plans[i % len(plans)].run()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(K):
+        p = plans[i % len(plans)]
+        ev[i][0].record()
+        p.run_splits()
+        ev[i][1].record()
+        p.run_merge()
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / K
+    split_us = sum(e[0].elapsed_time(e[1]) for e in ev) / K * 1e3
+    merge_us = sum(e[1].elapsed_time(e[2]) for e in ev) / K * 1e3
+    log(f"{ms_per_step * 1e3:.1f} us/step (splits {split_us:.1f} us, merge {merge_us:.1f} us)")
+
+    achieved = nb["total"] / (split_us * 1e-6) / 1e9
+    packed_gbps = nb["packed"] / (split_us * 1e-6) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"decode_{args.config}_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    result = {
+        "metric": "decode-attn µs/layer + achieved HBM GB/s (% peak), 32Q/8KV d128 b16 32K ctx"
+        if args.config == "cfg3" else f"decode-attn us/layer-step ({args.config})",
+        "value": round(ms_per_step * 1e3, 2),
+        "unit": "us/layer-step",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: fp16 N(0,1) K/V with x{:g} outlier key channels, quantised on device".format(
+            cfg["outlier"]),
+        "config": {"workload": f"{args.config}: B{cfg['B']} Hq{cfg['Hq']} Hkv{cfg['Hkv']} d{D} ctx{cfg['ctx']} "
+                               f"S{S} G{G} {int(cfg['boost'] * 100 * 10) / 10}% INT4 keys, INT2 values",
+                   "batch": cfg["B"], "context": cfg["ctx"], "pages_per_seq": w["n_pages"],
+                   "tail_tokens": w["n_tail"], "pool_copies": len(plans), "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "kernel": "decode split-K (kitty_paged_decode_splits)",
+                     "kernel_us": round(split_us, 2), "merge_us": round(merge_us, 2),
+                     "algorithmic_bytes": nb["total"], "packed_kv_bytes": nb["packed"],
+                     "packed_kv_GBps": round(packed_gbps, 1),
+                     "packed_kv_frac": round(packed_gbps / HBM_PEAK_GBPS, 4)},
+    }
+    if not args.no_quantize:
+        result["quantize_pack"] = bench_quantize(torch, dev)
+    if not args.no_cpu_baseline:
+        log("timing CPU baseline (oracle port, 1 thread)")
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

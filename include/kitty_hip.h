@@ -1,0 +1,198 @@
+/*
+ * kitty_hip.h — C ABI of libkitty_hip.so, the MI355X (gfx950) implementation
+ * of Kitty's quantized-KV hot path.
+ *
+ * The reference (bitxwolf/kitty-kv) exposes this path as in-process Python
+ * calls on torch tensors; each entry point below replaces one of them and
+ * cites it.  The ABI is plain C: device pointers, sizes and strides, no torch
+ * types.  Conventions:
+ *   - every pointer argument is a device pointer unless stated otherwise;
+ *   - strides are in elements of the pointed-to type;
+ *   - fp16 data is passed as uint16_t bit patterns;
+ *   - calls are asynchronous on the given stream, never allocate device
+ *     memory and never synchronise;
+ *   - the return value is KITTY_OK or a negative KITTY_E_* code, and
+ *     kitty_last_error() (thread-local) describes the last failure.
+ */
+#ifndef KITTY_HIP_H
+#define KITTY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KITTY_ABI_VERSION 1
+
+#define KITTY_OK 0
+#define KITTY_E_INVALID (-1)     /* bad shape, stride, alignment or null pointer */
+#define KITTY_E_HIP (-2)         /* HIP runtime error while launching */
+#define KITTY_E_UNSUPPORTED (-3) /* valid for the reference but not built here */
+#define KITTY_E_EXHAUSTED (-4)   /* page pool has no free page (layout.py:179-184) */
+#define KITTY_E_NOT_FOUND (-5)   /* page not present (layout.py:225-226) */
+
+typedef struct ihipStream_t *kitty_stream_t; /* == hipStream_t; NULL = default stream */
+
+int kitty_abi_version(void);
+const char *kitty_last_error(void);
+
+/* ------------------------------------------------------------------ pools
+ * Where quantised pages are written.  Each of the five pools of
+ * PageCentricKVLayoutManager (kitty/layout.py:129-147) is addressed as
+ *   base + page*s_page + head*s_head + row*s_row (+ column, contiguous),
+ * so both the contiguous pools and single-page views (the out_* arguments of
+ * quantize_key_page / quantize_value_page) can be described.  Strides are in
+ * elements (bytes for the uint8 pools).
+ *   key_low   (P, H, D, G/4) u8      — Tensor_2bits, low 2 bits of every channel
+ *   key_high  (P, H, Dk, G/4) u8     — Tensor_High_2bits, high 2 bits of boosted channels
+ *   key_scale / key_zero  (P, H, D)  — rows 0 / 1 of key_metadata (P, H, 2, D) fp16
+ *   value     (P, H, G, D/4) u8      — value_pool, 4 channels per byte
+ *   value_scale / value_zero (P, H, G) — columns 0 / 1 of value_metadata (P, H, G, 2) fp16
+ */
+typedef struct {
+    uint8_t *key_low;
+    int64_t key_low_s_page, key_low_s_head, key_low_s_row;
+    uint8_t *key_high;
+    int64_t key_high_s_page, key_high_s_head, key_high_s_row;
+    uint16_t *key_scale;
+    uint16_t *key_zero;
+    int64_t key_meta_s_page, key_meta_s_head, key_meta_s_chan;
+    uint8_t *value;
+    int64_t value_s_page, value_s_head, value_s_row;
+    uint16_t *value_scale;
+    uint16_t *value_zero;
+    int64_t value_meta_s_page, value_meta_s_head, value_meta_s_tok;
+    int64_t num_pages;    /* pages addressable through the strides; blocks whose
+                             page id is outside [0, num_pages) are not written */
+    int32_t num_kv_heads; /* H */
+    int32_t head_dim;     /* D, multiple of 4 */
+    int32_t page_tokens;  /* G, multiple of 4 */
+    int32_t d_boost;      /* Dk = KittyConfig.d_boost */
+} kitty_page_store;
+
+/* ------------------------------------------------- batch quantize + pack
+ * Replaces the spill loop of KittyInferencePipeline._trigger_quantization
+ * (kitty/pipeline.py:202-250), which calls quantize_key_page
+ * (kitty/kernels/quantize_key.py:217-269) and quantize_value_page
+ * (kitty/kernels/quantize_value.py:197-227) once per (layer, head), with one
+ * launch for all blocks of a spill.
+ *
+ * Block (o, i), o < n_outer, i < n_inner, quantises the G x D fp16 block
+ *   key[o*key_s_outer + i*key_s_inner + t*key_s_tok + d*key_s_chan]
+ * per channel (INT4 when boost_idx[d] < sentinel, else INT2) and the value
+ * block (same indexing with value_*) per token, and writes them to
+ * page page_ids[o], head i of `store`.  Value rows t >= value_rows are
+ * quantised as zeros (the reference zero-pads val_qbuf, pipeline.py:240-243).
+ * key or value may be NULL to quantise only the other one.  boost_idx row of
+ * block (o, i) starts at boost_idx + o*boost_s_outer + i*boost_s_inner.
+ * Bit-exact with quantize_key_page_torch / quantize_value_page_torch: fp32
+ * min/max, range clamped to 1e-8, correctly rounded division, round half to
+ * even, clamp, fp16 round-to-nearest-even for the stored scale and zero. */
+typedef struct {
+    const uint16_t *key;
+    int64_t key_s_outer, key_s_inner, key_s_tok, key_s_chan;
+    const uint16_t *value;
+    int64_t value_s_outer, value_s_inner, value_s_tok, value_s_chan;
+    const uint8_t *boost_idx;
+    int64_t boost_s_outer, boost_s_inner;
+    const int32_t *page_ids; /* [n_outer], device */
+    int32_t n_outer, n_inner;
+    int32_t value_rows;
+    int32_t sentinel; /* KittyConfig.sentinel = min(d_boost + 1, 255) */
+} kitty_quant_batch;
+
+int kitty_quantize_kv_blocks(const kitty_page_store *store, const kitty_quant_batch *batch,
+                             kitty_stream_t stream);
+
+/* ------------------------------------------------ key page dequantize
+ * Replaces dequantize_key_page (kitty/kernels/dequantize_key.py:169-228) and
+ * dequantize_key_page_torch (:35-97):
+ * out[d*out_s_chan + t] = ((low | high<<2) - zero[d]) * scale[d], computed in
+ * fp32 and stored as fp32 (out_fp32 != 0, the _torch variant's result) or
+ * fp16, reading page `page`, head `head` of `store` and boost row
+ * `boost_idx` (D,). */
+int kitty_dequantize_key_page(const kitty_page_store *store, int64_t page, int32_t head,
+                              const uint8_t *boost_idx, void *out, int64_t out_s_chan, int32_t out_fp32,
+                              kitty_stream_t stream);
+
+/* ---------------------------------------------- value page dequantize
+ * Replaces dequantize_value_page_torch (kitty/kernels/quantize_value.py:97-133):
+ * out[t*out_s_tok + d] = (code - zero[t]) * scale[t] in fp32, stored as fp32
+ * (out_fp32 != 0) or fp16, for page `page`, head `head` of `store`. */
+int kitty_dequantize_value_page(const kitty_page_store *store, int64_t page, int32_t head, void *out,
+                                int64_t out_s_tok, int32_t out_fp32, kitty_stream_t stream);
+
+/* ------------------------------------------- paged decode attention
+ * Replaces paged_attention / paged_attention_reference
+ * (kitty/kernels/attention.py:46-189, 292-341), batched over B sequences.
+ *
+ * For sequence b and query head qh (KV head kh = qh / (Hq/Hkv), :177) the
+ * attended tokens are, in order:
+ *   sink_len[b] FP16 sinks, num_pages[b] quantised pages
+ *   (block_table[b*bt_stride + p], p < num_pages[b]), tail_len[b] FP16 tail
+ *   tokens (key tail = KittyInferencePipeline.key_qbuf, value tail =
+ *   val_local; the reference appends the tail only when it is non-empty and
+ *   requires equal key / value tail lengths, :163-165).
+ * out[b, qh] = softmax(q . K^T * sm_scale) V in fp16; zeros when a sequence
+ * has no tokens (:180-182).
+ *
+ * Pools must be the contiguous tensors of PageCentricKVLayoutManager (16-byte
+ * aligned bases); page ids are int32 and byte offsets are 64-bit, so a pool
+ * may fill the whole 288 GB of an MI355X.
+ * The workspace (device memory, size from kitty_decode_workspace_size) holds
+ * the split-K partial results; it is scratch the caller owns.
+ */
+typedef struct {
+    const uint16_t *ptr;
+    int64_t s_seq, s_head, s_tok; /* element strides; channel stride is 1 */
+} kitty_fp16_seg;
+
+typedef struct {
+    const uint16_t *q; /* (B, Hq, D) */
+    int64_t q_s_seq, q_s_head;
+    uint16_t *out; /* (B, Hq, D) */
+    int64_t out_s_seq, out_s_head;
+
+    const uint8_t *key_low;     /* (P, H, D, G/4) */
+    const uint8_t *key_high;    /* (P, H, Dk, G/4) */
+    const uint16_t *key_meta;   /* (P, H, 2, D) */
+    const uint8_t *value;       /* (P, H, G, D/4) */
+    const uint16_t *value_meta; /* (P, H, G, 2) */
+    int64_t num_pool_pages;     /* P: every page id must be < P */
+
+    const int32_t *block_table; /* (B, bt_stride) physical page ids */
+    int64_t bt_stride;
+    const int32_t *num_pages; /* (B,) */
+    const uint8_t *boost_idx; /* (Hkv, D) for this layer */
+
+    kitty_fp16_seg sink_k, sink_v, tail_k, tail_v;
+    const int32_t *sink_len; /* (B,) */
+    const int32_t *tail_len; /* (B,) */
+    int32_t sink_capacity;   /* tokens allocated per (seq, head) in sink_k/v; lengths are clamped to it */
+    int32_t tail_capacity;   /* same for tail_k/v */
+
+    int32_t batch, num_q_heads, num_kv_heads, head_dim, page_tokens, d_boost;
+    int32_t max_pages;       /* >= every num_pages[b]; sizes the split grid */
+    int32_t pages_per_split; /* 0 = choose automatically */
+    float sm_scale;          /* 1/sqrt(D) in the reference (:172) */
+
+    void *workspace;
+    size_t workspace_bytes;
+} kitty_decode_args;
+
+int kitty_decode_workspace_size(const kitty_decode_args *args, size_t *bytes);
+int kitty_paged_decode(const kitty_decode_args *args, kitty_stream_t stream);
+
+/* The two phases of kitty_paged_decode, for callers that interleave other
+ * work or time the phases: _splits writes the split-K partials to the
+ * workspace, _merge combines them into `out`.  Same arguments; _merge must
+ * follow _splits on the same stream with the same args. */
+int kitty_paged_decode_splits(const kitty_decode_args *args, kitty_stream_t stream);
+int kitty_paged_decode_merge(const kitty_decode_args *args, kitty_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KITTY_HIP_H */

@@ -1,0 +1,158 @@
+// C ABI entry points of libkitty_hip.so that are not kernel-specific:
+// version, error reporting, and the paged decode dispatcher.
+#include <string>
+
+#include "common.h"
+#include "decode.h"
+
+namespace kitty {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string &msg) { g_last_error = msg; }
+const char *get_error() { return g_last_error.c_str(); }
+
+// Split size: enough (b, kh, split) work items to cover the 256 CUs several
+// times over, but at least 4 pages per split so partials stay small.
+static int choose_pages_per_split(const kitty_decode_args &a)
+{
+    if (a.pages_per_split > 0)
+        return a.pages_per_split;
+    const int64_t pairs = (int64_t)a.batch * a.num_kv_heads;
+    const int64_t target_items = 2048;
+    int64_t splits = (target_items + pairs - 1) / (pairs > 0 ? pairs : 1);
+    if (splits < 1)
+        splits = 1;
+    int64_t pps = (a.max_pages + splits - 1) / splits;
+    if (pps < 4)
+        pps = 4;
+    return (int)pps;
+}
+
+static int build_params(const kitty_decode_args *args, DecodeParams &p)
+{
+    if (!args)
+        return fail(KITTY_E_INVALID, "args is NULL");
+    const kitty_decode_args &a = *args;
+    if (a.batch < 0 || a.num_q_heads <= 0 || a.num_kv_heads <= 0 || a.num_q_heads % a.num_kv_heads)
+        return fail(KITTY_E_INVALID, "num_q_heads must be a positive multiple of num_kv_heads");
+    if (a.head_dim <= 0 || a.head_dim % 4 || a.page_tokens <= 0 || a.page_tokens % 4)
+        return fail(KITTY_E_INVALID, "head_dim and page_tokens must be positive multiples of 4");
+    if (a.head_dim > 256 || a.page_tokens > kChunkMax)
+        return fail(KITTY_E_UNSUPPORTED, "head_dim <= 256 and page_tokens <= 256 are supported");
+    if (a.d_boost < 0 || a.d_boost > a.head_dim)
+        return fail(KITTY_E_INVALID, "d_boost must be in [0, head_dim]");
+    if (a.max_pages < 0 || a.pages_per_split < 0)
+        return fail(KITTY_E_INVALID, "max_pages and pages_per_split must be >= 0");
+    if (a.max_pages > 0 && (a.bt_stride < a.max_pages || !a.block_table || !a.key_low || !a.key_meta ||
+                            !a.value || !a.value_meta || (a.d_boost > 0 && !a.key_high)))
+        return fail(KITTY_E_INVALID, "pools and a block table with bt_stride >= max_pages are required");
+    p = DecodeParams{};
+    p.q = a.q;
+    p.q_s_seq = a.q_s_seq;
+    p.q_s_head = a.q_s_head;
+    p.out = a.out;
+    p.out_s_seq = a.out_s_seq;
+    p.out_s_head = a.out_s_head;
+    p.key_low = a.key_low;
+    p.key_high = a.key_high;
+    p.key_meta = a.key_meta;
+    p.value = a.value;
+    p.value_meta = a.value_meta;
+    p.num_pool_pages = a.num_pool_pages;
+    p.block_table = a.block_table;
+    p.bt_stride = a.bt_stride;
+    p.num_pages = a.num_pages;
+    p.boost_idx = a.boost_idx;
+    p.sink_k = a.sink_k;
+    p.sink_v = a.sink_v;
+    p.tail_k = a.tail_k;
+    p.tail_v = a.tail_v;
+    p.sink_len = a.sink_len;
+    p.tail_len = a.tail_len;
+    p.sink_cap = a.sink_capacity > 0 ? a.sink_capacity : 0;
+    p.tail_cap = a.tail_capacity > 0 ? a.tail_capacity : 0;
+    p.B = a.batch;
+    p.Hq = a.num_q_heads;
+    p.Hkv = a.num_kv_heads;
+    p.GQ = a.num_q_heads / a.num_kv_heads;
+    p.D = a.head_dim;
+    p.G = a.page_tokens;
+    p.Dk = a.d_boost;
+    p.max_pages = a.max_pages;
+    p.pages_per_split = choose_pages_per_split(a);
+    p.n_splits = (a.max_pages + p.pages_per_split - 1) / p.pages_per_split;
+    p.sm_scale = a.sm_scale;
+    return KITTY_OK;
+}
+
+static size_t workspace_bytes(const DecodeParams &p)
+{
+    const size_t rows = (size_t)p.B * p.Hq * (p.n_splits + 1);
+    return rows * p.D * sizeof(float) + rows * 2 * sizeof(float);
+}
+
+} // namespace kitty
+
+using namespace kitty;
+
+extern "C" int kitty_abi_version(void) { return KITTY_ABI_VERSION; }
+
+extern "C" const char *kitty_last_error(void) { return get_error(); }
+
+extern "C" int kitty_decode_workspace_size(const kitty_decode_args *args, size_t *bytes)
+{
+    DecodeParams p;
+    int rc = build_params(args, p);
+    if (rc)
+        return rc;
+    if (!bytes)
+        return fail(KITTY_E_INVALID, "bytes is NULL");
+    *bytes = workspace_bytes(p);
+    return KITTY_OK;
+}
+
+static int prepare(const kitty_decode_args *args, DecodeParams &p)
+{
+    int rc = build_params(args, p);
+    if (rc || p.B == 0)
+        return rc;
+    if (!args->q || !args->out || !args->num_pages || !args->boost_idx || !args->sink_len || !args->tail_len)
+        return fail(KITTY_E_INVALID, "NULL q, out, num_pages, boost_idx, sink_len or tail_len");
+    const size_t need = workspace_bytes(p);
+    if (!args->workspace || args->workspace_bytes < need)
+        return fail(KITTY_E_INVALID, "workspace too small: need " + std::to_string(need) + " bytes");
+    p.ws_o = (float *)args->workspace;
+    p.ws_ml = p.ws_o + (size_t)p.B * p.Hq * (p.n_splits + 1) * p.D;
+    return KITTY_OK;
+}
+
+extern "C" int kitty_paged_decode_splits(const kitty_decode_args *args, kitty_stream_t stream)
+{
+    DecodeParams p;
+    int rc = prepare(args, p);
+    if (rc || p.B == 0)
+        return rc;
+    return launch_splits(p, (hipStream_t)stream);
+}
+
+extern "C" int kitty_paged_decode_merge(const kitty_decode_args *args, kitty_stream_t stream)
+{
+    DecodeParams p;
+    int rc = prepare(args, p);
+    if (rc || p.B == 0)
+        return rc;
+    return launch_merge(p, (hipStream_t)stream);
+}
+
+extern "C" int kitty_paged_decode(const kitty_decode_args *args, kitty_stream_t stream)
+{
+    DecodeParams p;
+    int rc = prepare(args, p);
+    if (rc || p.B == 0)
+        return rc;
+    rc = launch_splits(p, (hipStream_t)stream);
+    if (rc)
+        return rc;
+    return launch_merge(p, (hipStream_t)stream);
+}

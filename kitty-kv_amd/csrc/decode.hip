@@ -1,0 +1,340 @@
+// Split-K paged decode attention over Kitty's dense-sparse pages (gfx950).
+//
+// Work decomposition (flash-decoding): for every (sequence b, KV head kh) the
+// quantised pages are cut into splits of `pages_per_split` pages; one extra
+// split per (b, kh) attends the FP16 sinks and tail.  Each split produces,
+// for every query head of the GQA group, an unnormalised partial
+// (O, m, l) in base-2 online-softmax form; a merge kernel combines the
+// n_splits + 1 partials of (b, qh) into the fp16 output.  The result equals
+// softmax(q K^T / sqrt(D)) V over sinks ‖ dequantised pages ‖ tail, which is
+// paged_attention_reference (kitty/kernels/attention.py:136-189).
+//
+// This file holds the shape-generic path (any D, G <= 256, multiples of 4):
+// pages are staged in LDS and dequantised with the reference's own formula
+// k = (code - z) * s, v = (code - z_t) * s_t in fp32.
+#include "common.h"
+#include "decode.h"
+
+namespace kitty {
+
+constexpr int kGenThreads = 256;
+
+// LDS for one generic workgroup, carved from dynamic shared memory.
+struct GenLds {
+    float *qs;     // [GQ][D]   q * sm_scale * log2(e)
+    float *O;      // [GQ][D]   running unnormalised output
+    float *m, *l;  // [GQ]
+    float *alpha;  // [GQ]
+    float *sc;     // [GQ][CH]  scores, then probabilities
+    float *red;    // [kGenThreads * GQ]
+    uint8_t *klow, *khigh, *vcode, *brow;
+    float *kscale, *kzero, *vscale, *vzero;
+};
+
+// Scores, online softmax and PV for one chunk of n tokens (n <= CH).
+// kval(d, t) / vval(t, d) return the fp32 key / value of token t.
+template <int GQ, typename KF, typename VF>
+__device__ void gen_chunk(const GenLds &s, int D, int n, KF kval, VF vval)
+{
+    const int tid = threadIdx.x;
+    // --- scores: thread (t, slice) sums a contiguous channel range
+    {
+        const int nsl = kGenThreads / n;
+        const int t = tid % n, sl = tid / n;
+        const int dps = (D + nsl - 1) / nsl;
+        float acc[GQ];
+#pragma unroll
+        for (int g = 0; g < GQ; ++g)
+            acc[g] = 0.0f;
+        if (sl < nsl) {
+            const int d0 = min(D, sl * dps), d1 = min(D, d0 + dps);
+            for (int d = d0; d < d1; ++d) {
+                const float k = kval(d, t);
+#pragma unroll
+                for (int g = 0; g < GQ; ++g)
+                    acc[g] += s.qs[g * D + d] * k;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GQ; ++g)
+            s.red[g * kGenThreads + tid] = acc[g];
+        __syncthreads();
+        for (int e = tid; e < GQ * n; e += kGenThreads) {
+            const int g = e / n, tt = e - g * n;
+            float v = 0.0f;
+            for (int s2 = 0; s2 < nsl; ++s2)
+                v += s.red[g * kGenThreads + s2 * n + tt];
+            s.sc[g * kChunkMax + tt] = v;
+        }
+        __syncthreads();
+    }
+    // --- online softmax, one wave per head (round robin)
+    {
+        const int wave = tid / 64, lane = tid % 64;
+        for (int g = wave; g < GQ; g += kGenThreads / 64) {
+            float mx = -__builtin_inff();
+            for (int t = lane; t < n; t += 64)
+                mx = fmaxf(mx, s.sc[g * kChunkMax + t]);
+            for (int off = 32; off > 0; off >>= 1)
+                mx = fmaxf(mx, __shfl_xor(mx, off));
+            const float m_old = s.m[g];
+            const float m_new = fmaxf(m_old, mx);
+            float sum = 0.0f;
+            for (int t = lane; t < n; t += 64) {
+                const float p = exp2f(s.sc[g * kChunkMax + t] - m_new);
+                s.sc[g * kChunkMax + t] = p;
+                sum += p;
+            }
+            for (int off = 32; off > 0; off >>= 1)
+                sum += __shfl_xor(sum, off);
+            if (lane == 0) {
+                const float a = m_old == -__builtin_inff() ? 0.0f : exp2f(m_old - m_new);
+                s.alpha[g] = a;
+                s.l[g] = s.l[g] * a + sum;
+                s.m[g] = m_new;
+            }
+        }
+        __syncthreads();
+    }
+    // --- PV: thread (d, slice) sums a contiguous token range
+    {
+        const int nsl = kGenThreads / D;
+        const int d = tid % D, sl = tid / D;
+        const int tps = (n + nsl - 1) / nsl;
+        float acc[GQ];
+#pragma unroll
+        for (int g = 0; g < GQ; ++g)
+            acc[g] = 0.0f;
+        if (sl < nsl) {
+            const int t0 = min(n, sl * tps), t1 = min(n, t0 + tps);
+            for (int t = t0; t < t1; ++t) {
+                const float v = vval(t, d);
+#pragma unroll
+                for (int g = 0; g < GQ; ++g)
+                    acc[g] += s.sc[g * kChunkMax + t] * v;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GQ; ++g)
+            s.red[g * kGenThreads + tid] = acc[g];
+        __syncthreads();
+        for (int e = tid; e < GQ * D; e += kGenThreads) {
+            const int g = e / D, dd = e - g * D;
+            float v = 0.0f;
+            for (int s2 = 0; s2 < nsl; ++s2)
+                v += s.red[g * kGenThreads + s2 * D + dd];
+            s.O[e] = s.O[e] * s.alpha[g] + v;
+        }
+        __syncthreads();
+    }
+}
+
+// Copy n bytes global -> LDS with 4-byte accesses when both ends allow it.
+__device__ __forceinline__ void copy_bytes(uint8_t *dst, const uint8_t *src, int n)
+{
+    if ((((uintptr_t)src | (uintptr_t)n) & 3) == 0) {
+        const uint32_t *s4 = (const uint32_t *)src;
+        uint32_t *d4 = (uint32_t *)dst;
+        for (int e = threadIdx.x; e < n / 4; e += kGenThreads)
+            d4[e] = s4[e];
+    } else {
+        for (int e = threadIdx.x; e < n; e += kGenThreads)
+            dst[e] = src[e];
+    }
+}
+
+template <int GQ>
+__global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParams p)
+{
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int D = p.D, G = p.G, G4 = G / 4, D4 = D / 4, Dk = p.Dk, H = p.Hkv;
+    const int tid = threadIdx.x;
+
+    GenLds s;
+    unsigned char *ptr = smem;
+    auto carve = [&](size_t bytes) {
+        unsigned char *r = ptr;
+        ptr += (bytes + 15) & ~(size_t)15;
+        return r;
+    };
+    s.qs = (float *)carve(sizeof(float) * GQ * D);
+    s.O = (float *)carve(sizeof(float) * GQ * D);
+    s.m = (float *)carve(sizeof(float) * GQ);
+    s.l = (float *)carve(sizeof(float) * GQ);
+    s.alpha = (float *)carve(sizeof(float) * GQ);
+    s.sc = (float *)carve(sizeof(float) * GQ * kChunkMax);
+    s.red = (float *)carve(sizeof(float) * GQ * kGenThreads);
+    s.klow = (uint8_t *)carve((size_t)D * G4);
+    s.khigh = (uint8_t *)carve((size_t)Dk * G4 + 1);
+    s.vcode = (uint8_t *)carve((size_t)G * D4);
+    s.brow = (uint8_t *)carve(D);
+    s.kscale = (float *)carve(sizeof(float) * D);
+    s.kzero = (float *)carve(sizeof(float) * D);
+    s.vscale = (float *)carve(sizeof(float) * G);
+    s.vzero = (float *)carve(sizeof(float) * G);
+
+    const float qscale = p.sm_scale * kLog2e;
+    for (int e = tid; e < GQ * D; e += kGenThreads) {
+        const int g = e / D, d = e - g * D;
+        s.qs[e] = h2f(p.q[b * p.q_s_seq + (int64_t)(kh * GQ + g) * p.q_s_head + d]) * qscale;
+        s.O[e] = 0.0f;
+    }
+    if (tid < GQ) {
+        s.m[tid] = -__builtin_inff();
+        s.l[tid] = 0.0f;
+    }
+    for (int d = tid; d < D; d += kGenThreads)
+        s.brow[d] = p.boost_idx[kh * D + d];
+    __syncthreads();
+
+    bool poison = false;
+    if (split < p.n_splits) {
+        // ---------------------------------------------- quantised pages
+        const int np = p.num_pages[b];
+        if (np < 0 || np > p.max_pages)
+            poison = true;
+        const int p0 = split * p.pages_per_split;
+        const int p1 = poison ? p0 : min(np, p0 + p.pages_per_split);
+        for (int pi = p0; pi < p1; ++pi) {
+            const int32_t page = p.block_table[b * p.bt_stride + pi];
+            if (page < 0 || page >= p.num_pool_pages) {
+                poison = true;
+                break;
+            }
+            const int64_t ph = (int64_t)page * H + kh;
+            copy_bytes(s.klow, p.key_low + ph * D * G4, D * G4);
+            if (Dk > 0)
+                copy_bytes(s.khigh, p.key_high + ph * Dk * G4, Dk * G4);
+            copy_bytes(s.vcode, p.value + ph * G * D4, G * D4);
+            for (int e = tid; e < D; e += kGenThreads) {
+                s.kscale[e] = h2f(p.key_meta[ph * 2 * D + e]);
+                s.kzero[e] = h2f(p.key_meta[ph * 2 * D + D + e]);
+            }
+            for (int e = tid; e < G; e += kGenThreads) {
+                s.vscale[e] = h2f(p.value_meta[ph * 2 * G + 2 * e]);
+                s.vzero[e] = h2f(p.value_meta[ph * 2 * G + 2 * e + 1]);
+            }
+            __syncthreads();
+            // k = ((low | high << 2) - z) * s  (dequantize_key.py:73-95)
+            auto kval = [&](int d, int t) -> float {
+                int code = (s.klow[d * G4 + (t >> 2)] >> (2 * (t & 3))) & 3;
+                const int bi = s.brow[d];
+                if (bi < Dk)
+                    code |= ((s.khigh[bi * G4 + (t >> 2)] >> (2 * (t & 3))) & 3) << 2;
+                return ((float)code - s.kzero[d]) * s.kscale[d];
+            };
+            // v = (code - z_t) * s_t  (quantize_value.py:118-133)
+            auto vval = [&](int t, int d) -> float {
+                const int code = (s.vcode[t * D4 + (d >> 2)] >> (2 * (d & 3))) & 3;
+                return ((float)code - s.vzero[t]) * s.vscale[t];
+            };
+            // G <= kChunkMax, one chunk per page
+            gen_chunk<GQ>(s, D, G, kval, vval);
+        }
+    } else {
+        // ------------------------------------------ FP16 sinks then tail
+        const int ns = min(max(0, p.sink_len[b]), p.sink_cap), nt = min(max(0, p.tail_len[b]), p.tail_cap);
+        for (int seg = 0; seg < 2; ++seg) {
+            const kitty_fp16_seg &K = seg == 0 ? p.sink_k : p.tail_k;
+            const kitty_fp16_seg &V = seg == 0 ? p.sink_v : p.tail_v;
+            const int n = seg == 0 ? ns : nt;
+            const uint16_t *kb = K.ptr + b * K.s_seq + kh * K.s_head;
+            const uint16_t *vb = V.ptr + b * V.s_seq + kh * V.s_head;
+            for (int t0 = 0; t0 < n; t0 += kChunkMax) {
+                const int c = min(kChunkMax, n - t0);
+                auto kval = [&](int d, int t) -> float { return h2f(kb[(int64_t)(t0 + t) * K.s_tok + d]); };
+                auto vval = [&](int t, int d) -> float { return h2f(vb[(int64_t)(t0 + t) * V.s_tok + d]); };
+                gen_chunk<GQ>(s, D, c, kval, vval);
+            }
+        }
+    }
+    // ---------------------------------------------------- write partial
+    const int NS = p.n_splits + 1;
+    for (int e = tid; e < GQ * D; e += kGenThreads) {
+        const int g = e / D, d = e - g * D;
+        const int64_t row = ((int64_t)b * p.Hq + kh * GQ + g) * NS + split;
+        p.ws_o[row * D + d] = poison ? __builtin_nanf("") : s.O[e];
+    }
+    if (tid < GQ) {
+        const int64_t row = ((int64_t)b * p.Hq + kh * GQ + tid) * NS + split;
+        p.ws_ml[2 * row] = poison ? __builtin_nanf("") : s.m[tid];
+        p.ws_ml[2 * row + 1] = s.l[tid];
+    }
+}
+
+// Combine the n_splits + 1 partials of (b, qh) and write fp16 output.
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p)
+{
+    const int bq = blockIdx.x;
+    const int b = bq / p.Hq, qh = bq - b * p.Hq;
+    const int NS = p.n_splits + 1;
+    const int64_t row0 = (int64_t)bq * NS;
+    float M = -__builtin_inff();
+    bool nan = false;
+    for (int s2 = 0; s2 < NS; ++s2) {
+        const float m = p.ws_ml[2 * (row0 + s2)];
+        nan |= m != m;
+        M = fmaxf(M, m);
+    }
+    float L = 0.0f;
+    for (int s2 = 0; s2 < NS; ++s2) {
+        const float m = p.ws_ml[2 * (row0 + s2)];
+        if (m != -__builtin_inff())
+            L += p.ws_ml[2 * (row0 + s2) + 1] * exp2f(m - M);
+    }
+    for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
+        float acc = 0.0f;
+        for (int s2 = 0; s2 < NS; ++s2) {
+            const float m = p.ws_ml[2 * (row0 + s2)];
+            if (m != -__builtin_inff())
+                acc += p.ws_o[(row0 + s2) * p.D + d] * exp2f(m - M);
+        }
+        float o = L > 0.0f ? acc / L : 0.0f; // no tokens -> zeros (attention.py:180-182)
+        if (nan)
+            o = __builtin_nanf("");
+        p.out[b * p.out_s_seq + qh * p.out_s_head + d] = f2h(o);
+    }
+}
+
+size_t generic_lds_bytes(int GQ, int D, int G, int Dk)
+{
+    auto a = [](size_t x) { return (x + 15) & ~(size_t)15; };
+    return a(4 * GQ * D) * 2 + a(4 * GQ) * 3 + a(4 * GQ * kChunkMax) + a(4 * GQ * kGenThreads) +
+           a((size_t)D * (G / 4)) + a((size_t)Dk * (G / 4) + 1) + a((size_t)G * (D / 4)) + a(D) + a(4 * D) * 2 +
+           a(4 * G) * 2;
+}
+
+int launch_generic(const DecodeParams &p, hipStream_t stream)
+{
+    const size_t lds = generic_lds_bytes(p.GQ, p.D, p.G, p.Dk);
+    if (lds > 160 * 1024)
+        return fail(KITTY_E_UNSUPPORTED, "generic decode needs more than 160 KB of LDS for this shape");
+    dim3 grid(p.n_splits + 1, p.Hkv, p.B);
+    const void *fn = nullptr;
+    switch (p.GQ) {
+    case 1: fn = (const void *)decode_generic_kernel<1>; break;
+    case 2: fn = (const void *)decode_generic_kernel<2>; break;
+    case 4: fn = (const void *)decode_generic_kernel<4>; break;
+    case 8: fn = (const void *)decode_generic_kernel<8>; break;
+    case 16: fn = (const void *)decode_generic_kernel<16>; break;
+    default: return fail(KITTY_E_UNSUPPORTED, "num_q_heads / num_kv_heads must be 1, 2, 4, 8 or 16");
+    }
+    if (lds > 64 * 1024 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return fail(KITTY_E_HIP, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
+    void *kargs[] = {(void *)&p};
+    if (hipLaunchKernel(fn, grid, dim3(kGenThreads), kargs, lds, stream) != hipSuccess)
+        return fail(KITTY_E_HIP, "decode_generic_kernel launch failed");
+    return check_launch("decode_generic_kernel");
+}
+
+// Dispatch of the split phase: the generic kernel handles every shape.
+int launch_splits(const DecodeParams &p, hipStream_t stream) { return launch_generic(p, stream); }
+
+int launch_merge(const DecodeParams &p, hipStream_t stream)
+{
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(p.B * p.Hq), dim3(128), 0, stream, p);
+    return check_launch("decode_merge_kernel");
+}
+
+} // namespace kitty

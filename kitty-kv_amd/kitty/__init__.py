@@ -1,0 +1,16 @@
+"""Kitty 2-bit KV cache, MI355X (gfx950) implementation of the quantized-KV hot path.
+
+Public names follow the reference package (kitty/__init__.py:7-27).  All
+compute runs in libkitty_hip.so (hand-written HIP kernels for gfx950) on ROCm
+device tensors; there is no CPU compute path.
+"""
+from .config import KittyConfig
+from .layout import Page, PageCentricKVLayoutManager
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "KittyConfig",
+    "Page",
+    "PageCentricKVLayoutManager",
+]

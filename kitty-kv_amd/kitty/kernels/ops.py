@@ -1,0 +1,220 @@
+"""Torch-facing wrappers over the C ABI (include/kitty_hip.h).
+
+Every function here validates shapes/dtypes/devices on the host, builds the
+plain-C argument structs from tensor pointers and strides, and launches on the
+caller's current HIP stream.  Nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from .. import _hip
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check_fp16(name: str, t: torch.Tensor) -> None:
+    if t.dtype == torch.bfloat16:
+        raise NotImplementedError(f"{name}: bfloat16 buffers are not supported by the HIP kernels (fp16 only)")
+    _need(t.dtype == torch.float16, f"{name} must be float16, got {t.dtype}")
+
+
+def _dev_i32(values: Sequence[int], device: torch.device) -> torch.Tensor:
+    return torch.tensor(list(values), dtype=torch.int32).to(device, non_blocking=True)
+
+
+# ------------------------------------------------------------ page stores
+
+def pool_store(key_baseline: torch.Tensor, key_boost: torch.Tensor, key_meta: torch.Tensor,
+               value_pool: torch.Tensor, value_meta: torch.Tensor) -> _hip.PageStore:
+    """PageStore over the layout manager's five (P, H, ...) pools."""
+    P, H, D, G4 = key_baseline.shape
+    G = G4 * 4
+    Dk = key_boost.shape[2]
+    _need(key_baseline.dtype == torch.uint8 and key_boost.dtype == torch.uint8 and value_pool.dtype == torch.uint8,
+          "packed pools must be uint8")
+    _check_fp16("key_metadata", key_meta)
+    _check_fp16("value_metadata", value_meta)
+    _need(tuple(key_boost.shape[:2]) == (P, H) and key_boost.shape[3] == G4, "key_boost shape")
+    _need(tuple(key_meta.shape) == (P, H, 2, D), "key_metadata shape")
+    _need(tuple(value_pool.shape) == (P, H, G, D // 4), "value_pool shape")
+    _need(tuple(value_meta.shape) == (P, H, G, 2), "value_metadata shape")
+    for t in (key_baseline, key_boost, value_pool):
+        _need(t.stride(3) == 1, "packed pools need a contiguous last dimension")
+    s = _hip.PageStore()
+    s.key_low = key_baseline.data_ptr()
+    s.key_low_s_page, s.key_low_s_head, s.key_low_s_row = key_baseline.stride()[:3]
+    s.key_high = key_boost.data_ptr() if Dk > 0 else 0
+    s.key_high_s_page, s.key_high_s_head, s.key_high_s_row = key_boost.stride()[:3]
+    s.key_scale = key_meta.data_ptr()
+    s.key_zero = key_meta.data_ptr() + key_meta.stride(2) * 2
+    s.key_meta_s_page, s.key_meta_s_head = key_meta.stride(0), key_meta.stride(1)
+    s.key_meta_s_chan = key_meta.stride(3)
+    s.value = value_pool.data_ptr()
+    s.value_s_page, s.value_s_head, s.value_s_row = value_pool.stride()[:3]
+    s.value_scale = value_meta.data_ptr()
+    s.value_zero = value_meta.data_ptr() + value_meta.stride(3) * 2
+    s.value_meta_s_page, s.value_meta_s_head, s.value_meta_s_tok = value_meta.stride()[:3]
+    s.num_pages = P
+    s.num_kv_heads, s.head_dim, s.page_tokens, s.d_boost = H, D, G, Dk
+    return s
+
+
+def quantize_into_pools(store: _hip.PageStore, key: Optional[torch.Tensor], value: Optional[torch.Tensor],
+                        boost_idx: Optional[torch.Tensor], page_ids: torch.Tensor, sentinel: int,
+                        value_rows: Optional[int] = None) -> None:
+    """One launch over an (outer, inner=head) grid of fp16 blocks.
+
+    key / value: (n_outer, n_inner, G, D) fp16 views (any strides);
+    boost_idx: (n_outer, n_inner, D) or (n_inner, D) uint8; page_ids: (n_outer,)
+    int32 device tensor of destination pages.
+    """
+    ref = key if key is not None else value
+    _need(ref is not None, "nothing to quantise")
+    dev = _hip.require_device(key, value, boost_idx, page_ids)
+    n_outer, n_inner, G, D = ref.shape
+    _need(G == store.page_tokens and D == store.head_dim and n_inner == store.num_kv_heads,
+          "block shape does not match the pools")
+    _need(page_ids.dtype == torch.int32 and page_ids.numel() == n_outer, "page_ids must be int32 (n_outer,)")
+    b = _hip.QuantBatch()
+    if key is not None:
+        _check_fp16("key", key)
+        _need(tuple(key.shape) == (n_outer, n_inner, G, D), "key shape")
+        b.key = key.data_ptr()
+        b.key_s_outer, b.key_s_inner, b.key_s_tok, b.key_s_chan = key.stride()
+    if value is not None:
+        _check_fp16("value", value)
+        _need(tuple(value.shape) == (n_outer, n_inner, G, D), "value shape")
+        b.value = value.data_ptr()
+        b.value_s_outer, b.value_s_inner, b.value_s_tok, b.value_s_chan = value.stride()
+    if key is not None:
+        _need(boost_idx is not None and boost_idx.dtype == torch.uint8 and boost_idx.shape[-1] == D
+              and boost_idx.stride(-1) == 1, "boost_idx must be uint8 (..., D) with contiguous rows")
+        b.boost_idx = boost_idx.data_ptr()
+        if boost_idx.dim() == 3:
+            b.boost_s_outer, b.boost_s_inner = boost_idx.stride(0), boost_idx.stride(1)
+        else:
+            b.boost_s_outer, b.boost_s_inner = 0, boost_idx.stride(0)
+    b.page_ids = page_ids.data_ptr()
+    b.n_outer, b.n_inner = n_outer, n_inner
+    b.value_rows = G if value_rows is None else int(value_rows)
+    b.sentinel = int(sentinel)
+    L = _hip.load()
+    _hip.check(L.kitty_quantize_kv_blocks(ctypes.byref(store), ctypes.byref(b), _hip.stream_ptr(dev)))
+
+
+# --------------------------------------------------------------- decode
+
+class DecodePlan:
+    """Validated, pre-built arguments of one batched paged-decode call.
+
+    Building the plan does all host-side checks and allocates the workspace
+    once; ``run()`` then only enqueues the kernels on the current stream, so
+    a decode loop (or the benchmark) pays no Python validation per step.
+
+    q (B, Hq, D) fp16; block_table (B, W) int32; num_pages (B,) int32;
+    pools as in the layout manager; boost_idx (Hkv, D) uint8;
+    sink_k/v (B, Hkv, S, D) fp16 + sink_len (B,) int32;
+    tail_k/v (B, Hkv, T, D) fp16 + tail_len (B,) int32; out (B, Hq, D) fp16.
+    """
+
+    def __init__(self, q: torch.Tensor, block_table: torch.Tensor, num_pages: torch.Tensor,
+                 key_baseline: torch.Tensor, key_boost: torch.Tensor, key_meta: torch.Tensor,
+                 value_pool: torch.Tensor, value_meta: torch.Tensor, boost_idx: torch.Tensor,
+                 sink_k: torch.Tensor, sink_v: torch.Tensor, sink_len: torch.Tensor,
+                 tail_k: torch.Tensor, tail_v: torch.Tensor, tail_len: torch.Tensor,
+                 max_pages: Optional[int] = None, pages_per_split: int = 0,
+                 sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                 workspace: Optional[torch.Tensor] = None):
+        dev = _hip.require_device(q, block_table, num_pages, key_baseline, key_boost, key_meta, value_pool,
+                                  value_meta, boost_idx, sink_k, sink_v, sink_len, tail_k, tail_v, tail_len)
+        B, Hq, D = q.shape
+        P, Hkv, D2, G4 = key_baseline.shape
+        _need(D2 == D, "head_dim mismatch between q and pools")
+        _check_fp16("q", q)
+        for name, t in (("sink_k", sink_k), ("sink_v", sink_v), ("tail_k", tail_k), ("tail_v", tail_v)):
+            _check_fp16(name, t)
+            _need(t.dim() == 4 and t.shape[0] == B and t.shape[1] == Hkv and t.shape[3] == D and t.stride(3) == 1,
+                  f"{name} must be (B, Hkv, n, D) with contiguous channels")
+        _need(q.stride(2) == 1, "q channels must be contiguous")
+        _need(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == B
+              and block_table.stride(1) == 1, "block_table must be int32 (B, W) with contiguous rows")
+        for name, t in (("num_pages", num_pages), ("sink_len", sink_len), ("tail_len", tail_len)):
+            _need(t.dtype == torch.int32 and t.numel() == B and t.is_contiguous(), f"{name} must be int32 (B,)")
+        _need(boost_idx.dtype == torch.uint8 and tuple(boost_idx.shape) == (Hkv, D) and boost_idx.is_contiguous(),
+              "boost_idx must be contiguous uint8 (Hkv, D)")
+        for t in (key_baseline, key_boost, key_meta, value_pool, value_meta):
+            _need(t.is_contiguous(), "pools must be contiguous")
+        if max_pages is None:
+            max_pages = block_table.shape[1]
+        _need(max_pages <= block_table.shape[1], "max_pages exceeds the block table width")
+        if out is None:
+            out = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
+        _need(out.dtype == torch.float16 and tuple(out.shape) == (B, Hq, D) and out.stride(2) == 1, "out shape")
+
+        a = _hip.DecodeArgs()
+        a.q, a.q_s_seq, a.q_s_head = q.data_ptr(), q.stride(0), q.stride(1)
+        a.out, a.out_s_seq, a.out_s_head = out.data_ptr(), out.stride(0), out.stride(1)
+        a.key_low, a.key_high, a.key_meta = key_baseline.data_ptr(), key_boost.data_ptr(), key_meta.data_ptr()
+        a.value, a.value_meta = value_pool.data_ptr(), value_meta.data_ptr()
+        a.num_pool_pages = P
+        a.block_table, a.bt_stride = block_table.data_ptr(), block_table.stride(0)
+        a.num_pages, a.boost_idx = num_pages.data_ptr(), boost_idx.data_ptr()
+        for name, t in (("sink_k", sink_k), ("sink_v", sink_v), ("tail_k", tail_k), ("tail_v", tail_v)):
+            setattr(a, name, _hip.Fp16Seg(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2)))
+        a.sink_len, a.tail_len = sink_len.data_ptr(), tail_len.data_ptr()
+        a.sink_capacity, a.tail_capacity = sink_k.shape[2], tail_k.shape[2]
+        _need(sink_v.shape[2] == sink_k.shape[2] and tail_v.shape[2] >= tail_k.shape[2],
+              "sink_v / tail_v must hold as many tokens as sink_k / tail_k")
+        a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, D
+        a.page_tokens, a.d_boost = G4 * 4, key_boost.shape[2]
+        a.max_pages, a.pages_per_split = int(max_pages), int(pages_per_split)
+        a.sm_scale = float(1.0 / math.sqrt(D) if sm_scale is None else sm_scale)
+        self._L = _hip.load()
+        need = ctypes.c_size_t(0)
+        _hip.check(self._L.kitty_decode_workspace_size(ctypes.byref(a), ctypes.byref(need)))
+        if workspace is None or workspace.numel() * workspace.element_size() < need.value:
+            workspace = torch.empty(max(need.value, 16), dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        self.args = a
+        self.out = out
+        self.device = dev
+        # keep every tensor the kernels read alive as long as the plan
+        self._keep = (q, block_table, num_pages, key_baseline, key_boost, key_meta, value_pool, value_meta,
+                      boost_idx, sink_k, sink_v, sink_len, tail_k, tail_v, tail_len, workspace)
+
+    def run(self) -> torch.Tensor:
+        _hip.check(self._L.kitty_paged_decode(ctypes.byref(self.args), _hip.stream_ptr(self.device)))
+        return self.out
+
+    def run_splits(self) -> None:
+        _hip.check(self._L.kitty_paged_decode_splits(ctypes.byref(self.args), _hip.stream_ptr(self.device)))
+
+    def run_merge(self) -> torch.Tensor:
+        _hip.check(self._L.kitty_paged_decode_merge(ctypes.byref(self.args), _hip.stream_ptr(self.device)))
+        return self.out
+
+
+def paged_decode(*args, **kwargs) -> torch.Tensor:
+    """Batched fused paged decode attention: ``DecodePlan(*args, **kwargs).run()``."""
+    return DecodePlan(*args, **kwargs).run()
+
+
+def decode_workspace_bytes(B: int, Hq: int, Hkv: int, D: int, G: int, Dk: int, max_pages: int,
+                           pages_per_split: int = 0) -> int:
+    """Workspace size for paged_decode with these shapes (for preallocation)."""
+    a = _hip.DecodeArgs()
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, D
+    a.page_tokens, a.d_boost, a.max_pages, a.pages_per_split = G, Dk, max_pages, pages_per_split
+    a.bt_stride = max(1, max_pages)
+    a.block_table = a.key_low = a.key_meta = a.value = a.value_meta = a.key_high = 1  # non-null placeholders
+    need = ctypes.c_size_t(0)
+    _hip.check(_hip.load().kitty_decode_workspace_size(ctypes.byref(a), ctypes.byref(need)))
+    return need.value

@@ -1,0 +1,268 @@
+"""CPU oracle for the quantized-KV hot path of bitxwolf/kitty-kv.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker or as the timed CPU baseline.  The product package never imports it.
+
+Two independent restatements of the reference's PyTorch fallback live here:
+
+* ``libkitty_oracle.so`` (``kitty_oracle.c``, built by ``oracle/Makefile``): a
+  scalar C restatement, op for op, of
+  ``kitty/kernels/quantize_key.py:38-124``, ``quantize_value.py:38-133``,
+  ``dequantize_key.py:35-97`` and ``kitty/kernels/attention.py:46-189``.
+* ``*_np`` functions below: vectorised numpy restatements of the same
+  functions, written separately so that the C and numpy versions check each
+  other bit for bit.
+
+Parity pins (tests/test_oracle.py): the reference's two known-answer tests
+(``tests/test_quantize.py:141-166`` and ``:247-268``), its round-trip bounds
+(``:56-113``, ``:206-230``), hand-derived tie and underflow cases, brute force
+over every 4-token code pattern at G=4, and the paged attention checked against
+torch's ``scaled_dot_product_attention`` on the oracle's dequantised K/V.
+Only the sign of a zero zero-point and the reference's fp32 summation order
+are unpinned; both are compared by value / within tolerance.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libkitty_oracle.so")
+_lib: Optional[ctypes.CDLL] = None
+
+
+def build(force: bool = False) -> str:
+    """Compile the C oracle with ``make`` (gcc, no fast-math, no contraction)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        I = ctypes.c_int
+        L.kitty_oracle_quantize_key.argtypes = [P, P, I, I, I, I, P, P, P, P]
+        L.kitty_oracle_quantize_value.argtypes = [P, I, I, P, P, P]
+        L.kitty_oracle_dequantize_key.argtypes = [P, P, P, P, P, I, I, I, P]
+        L.kitty_oracle_dequantize_value.argtypes = [P, P, P, I, I, P]
+        L.kitty_oracle_paged_attention.argtypes = [
+            P, P, I, P, P, P, P, P, P, I, P, P, I, P, P, I, I, I, I, I, I, P]
+        L.kitty_oracle_h2f.argtypes = [ctypes.c_uint16]
+        L.kitty_oracle_h2f.restype = ctypes.c_float
+        L.kitty_oracle_f2h.argtypes = [ctypes.c_float]
+        L.kitty_oracle_f2h.restype = ctypes.c_uint16
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f16bits(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float16)).view(np.uint16)
+
+
+# --------------------------------------------------------------- C oracle
+
+def quantize_key(key: np.ndarray, boost_idx: np.ndarray, d_boost: int, sentinel: int):
+    """key (D, G) fp16 -> (t2b (D,G/4) u8, thigh (d_boost,G/4) u8, scale (D,) f16, zero (D,) f16).
+
+    Restates ``quantize_key_page_torch`` (kitty/kernels/quantize_key.py:38-124)."""
+    kb = _f16bits(key)
+    D, G = kb.shape
+    bi = np.ascontiguousarray(boost_idx, dtype=np.uint8)
+    t2b = np.zeros((D, G // 4), np.uint8)
+    thigh = np.zeros((max(d_boost, 0), G // 4), np.uint8)
+    sc = np.zeros(D, np.uint16)
+    zp = np.zeros(D, np.uint16)
+    lib().kitty_oracle_quantize_key(_p(kb), _p(bi), D, G, d_boost, sentinel,
+                                    _p(t2b), _p(thigh), _p(sc), _p(zp))
+    return t2b, thigh, sc.view(np.float16), zp.view(np.float16)
+
+
+def quantize_value(value: np.ndarray):
+    """value (G, D) fp16 -> (packed (G, D/4) u8, scale (G,) f16, zero (G,) f16).
+
+    Restates ``quantize_value_page_torch`` (kitty/kernels/quantize_value.py:38-90)."""
+    vb = _f16bits(value)
+    G, D = vb.shape
+    packed = np.zeros((G, D // 4), np.uint8)
+    sc = np.zeros(G, np.uint16)
+    zp = np.zeros(G, np.uint16)
+    lib().kitty_oracle_quantize_value(_p(vb), G, D, _p(packed), _p(sc), _p(zp))
+    return packed, sc.view(np.float16), zp.view(np.float16)
+
+
+def dequantize_key(t2b, thigh, scale, zero, boost_idx, d_boost: int) -> np.ndarray:
+    """Restates ``dequantize_key_page_torch`` (kitty/kernels/dequantize_key.py:35-97); (D, G) fp32."""
+    t2b = np.ascontiguousarray(t2b, np.uint8)
+    D, G4 = t2b.shape
+    thigh = np.ascontiguousarray(thigh, np.uint8)
+    if thigh.size == 0:
+        thigh = np.zeros((1, G4), np.uint8)
+    out = np.zeros((D, G4 * 4), np.float32)
+    lib().kitty_oracle_dequantize_key(_p(t2b), _p(thigh), _p(_f16bits(scale)), _p(_f16bits(zero)),
+                                      _p(np.ascontiguousarray(boost_idx, np.uint8)), D, G4 * 4,
+                                      d_boost, _p(out))
+    return out
+
+
+def dequantize_value(packed, scale, zero) -> np.ndarray:
+    """Restates ``dequantize_value_page_torch`` (kitty/kernels/quantize_value.py:97-133); (G, D) fp32."""
+    packed = np.ascontiguousarray(packed, np.uint8)
+    G, D4 = packed.shape
+    out = np.zeros((G, D4 * 4), np.float32)
+    lib().kitty_oracle_dequantize_value(_p(packed), _p(_f16bits(scale)), _p(_f16bits(zero)),
+                                        G, D4 * 4, _p(out))
+    return out
+
+
+def paged_attention(q, page_list: Sequence[int], key_baseline, key_boost, key_meta,
+                    value_pool, value_meta, boost_idx, d_boost: int,
+                    sink_k, sink_v, tail_k, tail_v, num_q_heads: int, num_kv_heads: int,
+                    head_dim: int, n_threads: int = 0) -> np.ndarray:
+    """One sequence of ``paged_attention_reference`` (kitty/kernels/attention.py:46-189).
+
+    Pools are numpy arrays with the layout manager's shapes (layout.py:129-147);
+    q (Hq, D) fp16; sinks / tails (H, n, D) fp16 (tail attended iff n > 0).
+    Returns (Hq, D) fp16."""
+    P, H, D, G4 = key_baseline.shape
+    G = G4 * 4
+    assert H == num_kv_heads and D == head_dim
+    kb = np.ascontiguousarray(key_baseline, np.uint8)
+    kh = np.ascontiguousarray(key_boost, np.uint8)
+    if kh.size == 0:
+        kh = np.zeros((1,), np.uint8)
+    km = _f16bits(key_meta)
+    vp = np.ascontiguousarray(value_pool, np.uint8)
+    vm = _f16bits(value_meta)
+    pl = np.ascontiguousarray(np.asarray(page_list, dtype=np.int32))
+    if pl.size == 0:
+        pl = np.zeros(1, np.int32)
+    n_pages = len(page_list)
+    sk, sv = _f16bits(sink_k), _f16bits(sink_v)
+    tk, tv = _f16bits(tail_k), _f16bits(tail_v)
+    n_sink = sk.shape[1] if sk.ndim == 3 else 0
+    n_tail = tk.shape[1] if tk.ndim == 3 else 0
+    if sk.size == 0:
+        sk = sv = np.zeros(1, np.uint16)
+    if tk.size == 0:
+        tk = tv = np.zeros(1, np.uint16)
+    out = np.zeros((num_q_heads, D), np.uint16)
+    if n_threads <= 0:
+        n_threads = min(num_kv_heads, os.cpu_count() or 1)
+    lib().kitty_oracle_paged_attention(
+        _p(_f16bits(q)), _p(pl), n_pages, _p(kb), _p(kh), _p(km), _p(vp), _p(vm),
+        _p(np.ascontiguousarray(boost_idx, np.uint8)), d_boost,
+        _p(sk), _p(sv), n_sink, _p(tk), _p(tv), n_tail,
+        num_q_heads, num_kv_heads, D, G, n_threads, _p(out))
+    return out.view(np.float16)
+
+
+# ------------------------------------------------- numpy restatements
+
+def quantize_key_np(key: np.ndarray, boost_idx: np.ndarray, d_boost: int, sentinel: int):
+    """Vectorised numpy restatement of ``quantize_key_page_torch``
+    (kitty/kernels/quantize_key.py:69-124); same outputs as :func:`quantize_key`."""
+    x = np.asarray(key, np.float16).astype(np.float32)
+    D, G = x.shape
+    boosted = np.asarray(boost_idx).astype(np.int64) < sentinel
+    mn = x.min(axis=1)
+    mx = x.max(axis=1)
+    rng = np.maximum(mx - mn, np.float32(1e-8))
+    mq = np.where(boosted, np.float32(15.0), np.float32(3.0)).astype(np.float32)
+    s = (rng / mq).astype(np.float32)
+    zp = np.minimum(np.maximum(np.rint(-mn / s), np.float32(0)), mq).astype(np.float32)
+    qf = np.rint(x / s[:, None]) + zp[:, None]
+    c = np.minimum(np.maximum(qf, np.float32(0)), mq[:, None]).astype(np.uint8)
+    lo = c & 3
+    hi = (c >> 2) & 3
+    t2b = np.zeros((D, G // 4), np.uint8)
+    for i in range(4):
+        t2b |= (lo[:, i::4] << (2 * i)).astype(np.uint8)
+    thigh = np.zeros((d_boost, G // 4), np.uint8)
+    bi = np.asarray(boost_idx).astype(np.int64)
+    for d in np.nonzero(boosted)[0]:
+        if bi[d] < d_boost:
+            for i in range(4):
+                thigh[bi[d]] |= (hi[d, i::4] << (2 * i)).astype(np.uint8)
+    return t2b, thigh, s.astype(np.float16), zp.astype(np.float16)
+
+
+def quantize_value_np(value: np.ndarray):
+    """Vectorised numpy restatement of ``quantize_value_page_torch``
+    (kitty/kernels/quantize_value.py:58-90)."""
+    v = np.asarray(value, np.float16).astype(np.float32)
+    G, D = v.shape
+    mn = v.min(axis=1)
+    mx = v.max(axis=1)
+    rng = np.maximum(mx - mn, np.float32(1e-8))
+    s = (rng / np.float32(3.0)).astype(np.float32)
+    zp = np.minimum(np.maximum(np.rint(-mn / s), np.float32(0)), np.float32(3)).astype(np.float32)
+    c = np.minimum(np.maximum(np.rint(v / s[:, None]) + zp[:, None], np.float32(0)),
+                   np.float32(3)).astype(np.uint8)
+    packed = np.zeros((G, D // 4), np.uint8)
+    for i in range(4):
+        packed |= (c[:, i::4] << (2 * i)).astype(np.uint8)
+    return packed, s.astype(np.float16), zp.astype(np.float16)
+
+
+def dequantize_key_np(t2b, thigh, scale, zero, boost_idx, d_boost: int) -> np.ndarray:
+    t2b = np.asarray(t2b, np.uint8)
+    D, G4 = t2b.shape
+    shifts = np.array([0, 2, 4, 6], np.uint8)
+    lo = ((t2b[:, :, None] >> shifts) & 3).reshape(D, G4 * 4).astype(np.int32)
+    hi = np.zeros_like(lo)
+    bi = np.asarray(boost_idx).astype(np.int64)
+    for d in range(D):
+        if bi[d] < d_boost:
+            hi[d] = ((np.asarray(thigh, np.uint8)[bi[d]][:, None] >> shifts) & 3).reshape(-1)
+    xq = (lo | (hi << 2)).astype(np.float32)
+    s = np.asarray(scale, np.float16).astype(np.float32)[:, None]
+    z = np.asarray(zero, np.float16).astype(np.float32)[:, None]
+    return ((xq - z) * s).astype(np.float32)
+
+
+def dequantize_value_np(packed, scale, zero) -> np.ndarray:
+    packed = np.asarray(packed, np.uint8)
+    G, D4 = packed.shape
+    shifts = np.array([0, 2, 4, 6], np.uint8)
+    c = ((packed[:, :, None] >> shifts) & 3).reshape(G, D4 * 4).astype(np.float32)
+    s = np.asarray(scale, np.float16).astype(np.float32)[:, None]
+    z = np.asarray(zero, np.float16).astype(np.float32)[:, None]
+    return ((c - z) * s).astype(np.float32)
+
+
+def dequantized_kv(page_list, key_baseline, key_boost, key_meta, value_pool, value_meta,
+                   boost_idx, d_boost, sink_k, sink_v, tail_k, tail_v):
+    """Concatenated fp32 K, V per KV head as ``paged_attention_reference`` builds
+    them (kitty/kernels/attention.py:136-168): list of (T, D) arrays per head."""
+    P, H, D, G4 = key_baseline.shape
+    Ks, Vs = [], []
+    for h in range(H):
+        kp, vp_ = [], []
+        if sink_k.shape[1] > 0:
+            kp.append(np.asarray(sink_k[h], np.float16).astype(np.float32))
+            vp_.append(np.asarray(sink_v[h], np.float16).astype(np.float32))
+        for p in page_list:
+            kp.append(dequantize_key_np(key_baseline[p, h], key_boost[p, h], key_meta[p, h, 0],
+                                        key_meta[p, h, 1], boost_idx[h], d_boost).T)
+            vp_.append(dequantize_value_np(value_pool[p, h], value_meta[p, h, :, 0],
+                                           value_meta[p, h, :, 1]))
+        if tail_k.shape[1] > 0:
+            kp.append(np.asarray(tail_k[h], np.float16).astype(np.float32))
+            vp_.append(np.asarray(tail_v[h], np.float16).astype(np.float32))
+        Ks.append(np.concatenate(kp, 0) if kp else np.zeros((0, D), np.float32))
+        Vs.append(np.concatenate(vp_, 0) if vp_ else np.zeros((0, D), np.float32))
+    return Ks, Vs

@@ -1,0 +1,74 @@
+"""CPU checks of the C ABI: the library loads, exports every function that
+include/kitty_hip.h declares, and rejects bad arguments before touching a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    text = open(os.path.join(ROOT, "include", "kitty_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kitty_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared_functions()
+    for n in ("kitty_abi_version", "kitty_last_error", "kitty_quantize_kv_blocks", "kitty_paged_decode",
+              "kitty_decode_workspace_size", "kitty_dequantize_key_page", "kitty_dequantize_value_page"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from kitty import _hip
+    L = _hip.load()
+    for name in _declared_functions():
+        assert hasattr(L, name), name
+    assert set(_hip.EXPORTED_SYMBOLS) <= set(_declared_functions())
+    assert L.kitty_abi_version() == _hip.KITTY_ABI_VERSION
+
+
+def test_invalid_arguments_are_rejected_without_launch():
+    from kitty import _hip
+    L = _hip.load()
+    assert L.kitty_quantize_kv_blocks(None, None, None) == _hip.KITTY_E_INVALID
+    assert b"NULL" in L.kitty_last_error()
+    st = _hip.PageStore()
+    st.head_dim, st.page_tokens, st.num_kv_heads = 130, 128, 1
+    b = _hip.QuantBatch()
+    assert L.kitty_quantize_kv_blocks(ctypes.byref(st), ctypes.byref(b), None) == _hip.KITTY_E_INVALID
+    a = _hip.DecodeArgs()
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.page_tokens = 1, 6, 4, 128, 128
+    assert L.kitty_paged_decode(ctypes.byref(a), None) == _hip.KITTY_E_INVALID
+    a.num_q_heads, a.head_dim = 8, 512
+    assert L.kitty_paged_decode(ctypes.byref(a), None) == _hip.KITTY_E_UNSUPPORTED
+    with pytest.raises(NotImplementedError):
+        _hip.check(_hip.KITTY_E_UNSUPPORTED)
+    with pytest.raises(RuntimeError):
+        _hip.check(_hip.KITTY_E_EXHAUSTED)
+    with pytest.raises(KeyError):
+        _hip.check(_hip.KITTY_E_NOT_FOUND)
+
+
+def test_workspace_size_formula():
+    from kitty.kernels.ops import decode_workspace_bytes
+    # config 3: 16 x 8 pairs, 255 pages -> 16 splits of 16 pages (+1 FP16 split)
+    n = decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255)
+    assert n == 16 * 32 * 17 * (128 + 2) * 4
+
+
+def test_cpu_tensors_rejected_no_fallback():
+    import torch
+    from kitty.kernels import quantize_value_page_torch, paged_attention
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        quantize_value_page_torch(torch.zeros(8, 16, dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        z8 = torch.zeros(1, 1, 16, 2, dtype=torch.uint8)
+        paged_attention(torch.zeros(1, 16, dtype=torch.float16), [], z8, z8[:, :, :0], torch.zeros(1, 1, 2, 16).half(),
+                        torch.zeros(1, 1, 8, 4, dtype=torch.uint8), torch.zeros(1, 1, 8, 2).half(),
+                        torch.zeros(1, 16, dtype=torch.uint8), 0, torch.zeros(1, 0, 16).half(),
+                        torch.zeros(1, 0, 16).half(), torch.zeros(1, 0, 16).half(), torch.zeros(1, 0, 16).half(),
+                        1, 1, 16)

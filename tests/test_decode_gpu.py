@@ -1,0 +1,155 @@
+"""GPU parity of the fused split-K paged decode against the CPU oracle
+(paged_attention_reference restated, kitty/kernels/attention.py:46-189).
+
+Bar: |out - oracle| <= 2e-3 + 1e-2 * |oracle| elementwise.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from kvgen import random_pools, ragged_lengths
+from test_oracle import make_paged_case
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def _close(got, ref, what=""):
+    got = np.asarray(got, np.float32)
+    ref = np.asarray(ref, np.float32)
+    err = np.abs(got - ref) - (ATOL + RTOL * np.abs(ref))
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    assert (err <= 0).all(), f"{what}: max excess {err.max():.3g} (max |diff| {np.abs(got - ref).max():.3g})"
+
+
+def _to(dev, *arrs):
+    return [torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in arrs]
+
+
+@pytest.mark.parametrize("H,Hq,D,G,dk,n_pages,n_sink,n_tail", [
+    (2, 2, 16, 8, 4, 3, 4, 5),      # reference test config (tests/test_attention.py:24-36)
+    (2, 8, 16, 8, 4, 2, 0, 3),
+    (1, 4, 16, 8, 4, 0, 3, 0),      # sinks only (test_attention.py:190-215)
+    (2, 4, 128, 128, 16, 5, 32, 96),
+    (8, 8, 128, 128, 16, 7, 32, 96),  # config 1 shape: ctx 1024 = 32 + 7*128 + 96
+    (2, 16, 128, 128, 32, 3, 7, 0),
+    (2, 4, 64, 32, 8, 6, 1, 31),
+])
+def test_paged_attention_single_sequence(dev, H, Hq, D, G, dk, n_pages, n_sink, n_tail):
+    from kitty.kernels import paged_attention
+    rng = np.random.default_rng(H * 100 + Hq + D)
+    c = make_paged_case(rng, H, Hq, D, G, dk, n_pages, n_sink, n_tail)
+    ref = O.paged_attention(c["q"], c["pages"], c["kb"], c["kh"], c["km"], c["vp"], c["vm"], c["bi"], dk,
+                            c["sk"], c["sv"], c["tk"], c["tv"], Hq, H, D)
+    q, kb, kh, km, vp, vm, bi, sk, sv, tk, tv = _to(dev, c["q"], c["kb"], c["kh"], c["km"], c["vp"], c["vm"],
+                                                   c["bi"], c["sk"], c["sv"], c["tk"], c["tv"])
+    out = paged_attention(q, [int(p) for p in c["pages"]], kb, kh, km, vp, vm, bi, dk, sk, sv, tk, tv, Hq, H, D)
+    assert out.shape == (Hq, D) and out.dtype == torch.float16
+    _close(out.cpu().numpy(), ref, "single")
+
+
+def test_empty_context_gives_zeros(dev):
+    from kitty.kernels import paged_attention
+    rng = np.random.default_rng(0)
+    c = make_paged_case(rng, 2, 4, 16, 8, 4, 0, 0, 0)
+    q, kb, kh, km, vp, vm, bi, sk, sv, tk, tv = _to(dev, c["q"], c["kb"], c["kh"], c["km"], c["vp"], c["vm"],
+                                                   c["bi"], c["sk"], c["sv"], c["tk"], c["tv"])
+    out = paged_attention(q, [], kb, kh, km, vp, vm, bi, 4, sk, sv, tk, tv, 4, 2, 16)
+    assert (out.float() == 0).all()
+
+
+def test_tail_length_mismatch_raises(dev):
+    from kitty.kernels import paged_attention
+    rng = np.random.default_rng(0)
+    c = make_paged_case(rng, 2, 2, 16, 8, 4, 1, 4, 5)
+    q, kb, kh, km, vp, vm, bi, sk, sv, tk, tv = _to(dev, c["q"], c["kb"], c["kh"], c["km"], c["vp"], c["vm"],
+                                                   c["bi"], c["sk"], c["sv"], c["tk"], c["tv"])
+    with pytest.raises(RuntimeError, match="equal lengths"):
+        paged_attention(q, [int(c["pages"][0])], kb, kh, km, vp, vm, bi, 4, sk, sv, tk, tv[:, :3], 2, 2, 16)
+
+
+def _batched_case(dev, seed, B, Hq, H, D, G, dk, ctx, S=32, shuffle=True, pool_extra=7):
+    """Random-encoding pools, ctx[b] tokens per sequence = S sinks + pages + tail."""
+    gen = torch.Generator().manual_seed(seed)
+    sentinel = dk + 1
+    bi = torch.full((H, D), sentinel, dtype=torch.uint8)
+    for h in range(H):
+        bi[h, torch.randperm(D, generator=gen)[:dk]] = torch.arange(dk, dtype=torch.uint8)
+    n_pages = [(c - S) // G for c in ctx]
+    tails = [(c - S) % G for c in ctx]
+    P = sum(n_pages) + pool_extra
+    pools = random_pools(gen, P, H, D, G, dk, bi)
+    perm = torch.randperm(P, generator=gen) if shuffle else torch.arange(P)
+    W = max(max(n_pages), 1)
+    bt = torch.zeros(B, W, dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        bt[b, :n_pages[b]] = perm[off:off + n_pages[b]].to(torch.int32)
+        off += n_pages[b]
+    T = max(max(tails), 1)
+    q = torch.randn(B, Hq, D, generator=gen).half()
+    sk = torch.randn(B, H, S, D, generator=gen).half()
+    sv = torch.randn(B, H, S, D, generator=gen).half()
+    tk = torch.randn(B, H, T, D, generator=gen).half()
+    tv = torch.randn(B, H, T, D, generator=gen).half()
+    cpu = dict(q=q, bt=bt, n_pages=n_pages, tails=tails, pools=pools, bi=bi, sk=sk, sv=sv, tk=tk, tv=tv, S=S)
+    return cpu
+
+
+def _run_batched(dev, c, pages_per_split=0):
+    from kitty.kernels import paged_attention_batched
+    kb, kh, km, vp, vm = [t.to(dev) for t in c["pools"]]
+    B = c["q"].shape[0]
+    out = paged_attention_batched(
+        c["q"].to(dev), c["bt"].to(dev), torch.tensor(c["n_pages"], dtype=torch.int32, device=dev),
+        kb, kh, km, vp, vm, c["bi"].to(dev), c["sk"].to(dev), c["sv"].to(dev),
+        torch.full((B,), c["S"], dtype=torch.int32, device=dev), c["tk"].to(dev), c["tv"].to(dev),
+        torch.tensor(c["tails"], dtype=torch.int32, device=dev), pages_per_split=pages_per_split)
+    return out.cpu().numpy()
+
+
+def _oracle_batched(c, Hq, H, D, b):
+    kb, kh, km, vp, vm = [t.numpy() for t in c["pools"]]
+    n, t = c["n_pages"][b], c["tails"][b]
+    return O.paged_attention(c["q"][b].numpy(), c["bt"][b, :n].numpy(), kb, kh, km, vp, vm, c["bi"].numpy(),
+                             kh.shape[2], c["sk"][b].numpy(), c["sv"][b].numpy(), c["tk"][b, :, :t].numpy(),
+                             c["tv"][b, :, :t].numpy(), Hq, H, D)
+
+
+@pytest.mark.parametrize("pps", [0, 1, 3, 64])
+def test_batched_ragged_split_invariance(dev, pps):
+    """Config-4-like ragged batch (scaled down), shuffled pages; the result must
+    not depend on the split size."""
+    B, Hq, H, D, G, dk = 6, 32, 8, 128, 128, 32
+    ctx = [int(x) for x in ragged_lengths(4, B, 40, 3000)]
+    ctx[0] = 32   # sinks only
+    c = _batched_case(dev, 40, B, Hq, H, D, G, dk, ctx)
+    out = _run_batched(dev, c, pps)
+    for b in range(B):
+        _close(out[b], _oracle_batched(c, Hq, H, D, b), f"b={b} pps={pps}")
+
+
+@pytest.mark.parametrize("name,B,Hq,H,ctx,dk", [
+    ("config3", 16, 32, 8, 32768, 16),
+    ("config5", 4, 64, 8, 131072, 16),
+])
+def test_full_size_configs(dev, name, B, Hq, H, ctx, dk):
+    """BASELINE configs 3 and 5 at their full shapes against the oracle
+    (every sequence, every head)."""
+    D, G = 128, 128
+    c = _batched_case(dev, 3 if name == "config3" else 5, B, Hq, H, D, G, dk, [ctx] * B, pool_extra=11)
+    out = _run_batched(dev, c)
+    for b in range(B):
+        _close(out[b], _oracle_batched(c, Hq, H, D, b), f"{name} b={b}")
+
+
+def test_invalid_page_id_poisons_output(dev):
+    """A page id outside the pool is never dereferenced; the sequence's output becomes NaN."""
+    B, Hq, H, D, G, dk = 2, 4, 2, 128, 128, 16
+    c = _batched_case(dev, 9, B, Hq, H, D, G, dk, [32 + 3 * 128 + 5, 32 + 2 * 128])
+    c["bt"][1, 1] = 10 ** 6
+    out = _run_batched(dev, c)
+    assert np.isnan(out[1]).all()
+    _close(out[0], _oracle_batched(c, Hq, H, D, 0), "b=0")

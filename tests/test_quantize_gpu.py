@@ -1,0 +1,162 @@
+"""GPU parity of the batch quantize + pack kernel against the CPU oracle.
+
+Bar: packed codes bit-exact, scales and zero points equal by value (the sign
+of a zero zero-point is the only unpinned bit, see oracle/oracle.py).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from kvgen import calibrate_boost_idx, outlier_keys
+
+pytestmark = pytest.mark.gpu
+
+
+def _eq16(a, b):
+    return np.array_equal(np.asarray(a, np.float16).astype(np.float32), np.asarray(b, np.float16).astype(np.float32))
+
+
+def _pools(P, H, D, G, Dk, dev):
+    from kitty.kernels.ops import pool_store
+    kb = torch.full((P, H, D, G // 4), 0xAA, dtype=torch.uint8, device=dev)  # garbage: must be overwritten
+    kh = torch.full((P, H, Dk, G // 4), 0x55, dtype=torch.uint8, device=dev)
+    km = torch.full((P, H, 2, D), 7.0, dtype=torch.float16, device=dev)
+    vp = torch.full((P, H, G, D // 4), 0x33, dtype=torch.uint8, device=dev)
+    vm = torch.full((P, H, G, 2), 7.0, dtype=torch.float16, device=dev)
+    return (kb, kh, km, vp, vm), pool_store(kb, kh, km, vp, vm)
+
+
+def _check_page(pools, p, h, key_dg, value_gd, bi, Dk, sentinel, value_rows=None):
+    kb, kh, km, vp, vm = [t.cpu().numpy() for t in pools]
+    t2b, th, s, z = O.quantize_key(key_dg, bi, Dk, sentinel)
+    assert np.array_equal(kb[p, h], t2b), (p, h)
+    assert np.array_equal(kh[p, h], th), (p, h)
+    assert _eq16(km[p, h, 0], s) and _eq16(km[p, h, 1], z), (p, h)
+    if value_gd is not None:
+        v = value_gd.copy()
+        if value_rows is not None:
+            v[value_rows:] = 0
+        pk, sv, zv = O.quantize_value(v)
+        assert np.array_equal(vp[p, h], pk), (p, h)
+        assert _eq16(vm[p, h, :, 0], sv) and _eq16(vm[p, h, :, 1], zv), (p, h)
+
+
+def test_config2_quantize_pack_bit_exact(dev):
+    """4096 tokens x 8 KV heads x 128, 16 outlier key
+    channels per head x8, per-channel keys over G=128 groups, per-token values,
+    INT4 for the top 12.5% channels."""
+    from kitty.kernels.ops import quantize_into_pools
+    gen = torch.Generator().manual_seed(2)
+    T, H, D, G, Dk = 4096, 8, 128, 128, 16
+    sentinel = Dk + 1
+    K, chans = outlier_keys(gen, (T,), H, D, 16, 8.0)
+    V = torch.randn(T, H, D, generator=gen).half()
+    calib, _ = outlier_keys(gen, (256,), H, D, 16, 8.0, channels=chans)
+    bi = calibrate_boost_idx(calib, Dk, sentinel)
+    n_groups = T // G
+    P = n_groups + 5
+    pools, store = _pools(P, H, D, G, Dk, dev)
+    page_ids = torch.randperm(P, generator=gen)[:n_groups].to(torch.int32)
+    Kd, Vd = K.to(dev), V.to(dev)
+    kblocks = Kd.view(n_groups, G, H, D).permute(0, 2, 1, 3)   # (group, head, token, chan) strided
+    vblocks = Vd.view(n_groups, G, H, D).permute(0, 2, 1, 3)
+    quantize_into_pools(store, kblocks, vblocks, bi.to(dev), page_ids.to(dev), sentinel)
+    torch.cuda.synchronize()
+    Kn, Vn = K.numpy(), V.numpy()
+    for g in range(n_groups):
+        for h in range(H):
+            _check_page(pools, int(page_ids[g]), h, Kn[g * G:(g + 1) * G, h].T.copy(),
+                        Vn[g * G:(g + 1) * G, h].copy(), bi[h].numpy(), Dk, sentinel)
+
+
+@pytest.mark.parametrize("D,G,Dk,H", [(16, 8, 4, 2), (128, 128, 32, 4), (64, 32, 15, 1), (32, 16, 0, 3)])
+def test_small_shapes_and_edge_rows(dev, D, G, Dk, H):
+    from kitty.kernels.ops import quantize_into_pools
+    gen = torch.Generator().manual_seed(D * 7 + G)
+    sentinel = min(Dk + 1, 255)
+    n = 3
+    K = torch.randn(n, H, G, D, generator=gen)
+    K[0, 0, :, 1] = 2.5           # constant channel -> fp16 scale underflow
+    K[1, 0] = 0.0                 # all-zero block
+    K[2, -1, 0, :] = 0.5 * torch.arange(D)  # ties
+    K = K.half()
+    V = torch.randn(n, H, G, D, generator=gen).half()
+    V[0, 0, 3] = -1.0             # constant token
+    bi = torch.full((n, H, D), sentinel, dtype=torch.uint8)
+    for o in range(n):
+        for h in range(H):
+            perm = torch.randperm(D, generator=gen)[:Dk]
+            bi[o, h, perm] = torch.arange(Dk, dtype=torch.uint8)
+    pools, store = _pools(n + 1, H, D, G, Dk, dev)
+    page_ids = torch.tensor([2, 0, 3], dtype=torch.int32)
+    quantize_into_pools(store, K.to(dev), V.to(dev), bi.to(dev), page_ids.to(dev), sentinel)
+    torch.cuda.synchronize()
+    for o in range(n):
+        for h in range(H):
+            _check_page(pools, int(page_ids[o]), h, K[o, h].numpy().T.copy(), V[o, h].numpy(), bi[o, h].numpy(),
+                        Dk, sentinel)
+
+
+def test_value_rows_zero_padding(dev):
+    """Rows past value_rows quantise as zeros (pipeline.py:240-243)."""
+    from kitty.kernels.ops import quantize_into_pools
+    D, G, H = 128, 128, 2
+    gen = torch.Generator().manual_seed(11)
+    V = torch.randn(1, H, G, D, generator=gen).half()
+    pools, store = _pools(1, H, D, G, 16, dev)
+    quantize_into_pools(store, None, V.to(dev), None, torch.zeros(1, dtype=torch.int32, device=dev), 17,
+                        value_rows=37)
+    torch.cuda.synchronize()
+    vp, vm = pools[3].cpu().numpy(), pools[4].cpu().numpy()
+    for h in range(H):
+        v = V[0, h].numpy().copy()
+        v[37:] = 0
+        pk, sv, zv = O.quantize_value(v)
+        assert np.array_equal(vp[0, h], pk) and _eq16(vm[0, h, :, 0], sv) and _eq16(vm[0, h, :, 1], zv)
+
+
+def test_reference_signatures(dev):
+    """quantize_key_page / quantize_value_page / dequantize_* with the
+    reference's arguments, outputs written into strided pool views."""
+    from kitty.kernels import (quantize_key_page, quantize_value_page, quantize_key_page_torch,
+                               quantize_value_page_torch, dequantize_key_page_torch, dequantize_value_page_torch,
+                               dequantize_key_page)
+    D, G, Dk, H = 128, 128, 16, 2
+    gen = torch.Generator().manual_seed(5)
+    qbuf = torch.randn(H, G, D, generator=gen).half().to(dev)
+    bi = torch.full((D,), Dk + 1, dtype=torch.uint8)
+    bi[torch.randperm(D, generator=gen)[:Dk]] = torch.arange(Dk, dtype=torch.uint8)
+    bi = bi.to(dev)
+    kb = torch.zeros(4, H, D, G // 4, dtype=torch.uint8, device=dev)
+    kh = torch.zeros(4, H, Dk, G // 4, dtype=torch.uint8, device=dev)
+    km = torch.zeros(4, H, 2, D, dtype=torch.float16, device=dev)
+    vp = torch.zeros(4, H, G, D // 4, dtype=torch.uint8, device=dev)
+    vm = torch.zeros(4, H, G, 2, dtype=torch.float16, device=dev)
+    key_block = qbuf[1].T.contiguous()        # pipeline.py:219
+    quantize_key_page(key_block, bi, Dk, Dk + 1, kb[2, 1], kh[2, 1], km[2, 1, 0], km[2, 1, 1])
+    quantize_value_page(qbuf[0], vp[2, 1], vm[2, 1, :, 0], vm[2, 1, :, 1])   # strided scale/zero views
+    t2b, th, s, z = quantize_key_page_torch(key_block, bi, Dk, Dk + 1)
+    pk, sv, zv = quantize_value_page_torch(qbuf[0])
+    torch.cuda.synchronize()
+    e = O.quantize_key(key_block.cpu().numpy(), bi.cpu().numpy(), Dk, Dk + 1)
+    ev = O.quantize_value(qbuf[0].cpu().numpy())
+    assert np.array_equal(kb[2, 1].cpu().numpy(), e[0]) and np.array_equal(t2b.cpu().numpy(), e[0])
+    assert np.array_equal(kh[2, 1].cpu().numpy(), e[1]) and np.array_equal(th.cpu().numpy(), e[1])
+    assert _eq16(km[2, 1, 0].cpu(), e[2]) and _eq16(s.cpu(), e[2]) and _eq16(z.cpu(), e[3])
+    assert np.array_equal(vp[2, 1].cpu().numpy(), ev[0]) and np.array_equal(pk.cpu().numpy(), ev[0])
+    assert _eq16(vm[2, 1, :, 0].cpu(), ev[1]) and _eq16(vm[2, 1, :, 1].cpu(), ev[2]) and _eq16(zv.cpu(), ev[2])
+    assert kb[[0, 1, 3]].sum() == 0 and kb[2, 0].sum() == 0      # nothing else written
+    dk = dequantize_key_page_torch(t2b, th, s, z, bi, Dk)
+    assert np.array_equal(dk.cpu().numpy(), O.dequantize_key(*e, bi.cpu().numpy(), Dk))
+    dv = dequantize_value_page_torch(pk, sv, zv)
+    assert np.array_equal(dv.cpu().numpy(), O.dequantize_value(*ev))
+    out16 = torch.empty(D, G, dtype=torch.float16, device=dev)
+    dequantize_key_page(t2b, th, s, z, bi, Dk, out16)
+    assert np.array_equal(out16.cpu().numpy(), O.dequantize_key(*e, bi.cpu().numpy(), Dk).astype(np.float16))
+
+
+def test_cpu_tensors_are_rejected(dev):
+    from kitty.kernels import quantize_key_page_torch
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        quantize_key_page_torch(torch.zeros(16, 8, dtype=torch.float16), torch.zeros(16, dtype=torch.uint8), 4, 5)
