@@ -149,6 +149,13 @@ typedef struct {
     int64_t s_seq, s_head, s_tok; /* element strides; channel stride is 1 */
 } kitty_fp16_seg;
 
+/* Caller guarantees that every rank r < d_boost appears at most once in each
+ * boost_idx row (true for profiles from KittySensitivityProfiler, whose ranks
+ * come from one argsort, sensitivity.py:195-203).  Enables the MFMA kernel;
+ * without it the shape-generic kernel runs, which also reproduces the
+ * reference's behaviour for repeated ranks. */
+#define KITTY_DECODE_UNIQUE_BOOST_ROWS 1
+
 typedef struct {
     const uint16_t *q; /* (B, Hq, D) */
     int64_t q_s_seq, q_s_head;
@@ -176,6 +183,7 @@ typedef struct {
     int32_t batch, num_q_heads, num_kv_heads, head_dim, page_tokens, d_boost;
     int32_t max_pages;       /* >= every num_pages[b]; sizes the split grid */
     int32_t pages_per_split; /* 0 = choose automatically */
+    int32_t flags;           /* KITTY_DECODE_* bits */
     float sm_scale;          /* 1/sqrt(D) in the reference (:172) */
 
     void *workspace;

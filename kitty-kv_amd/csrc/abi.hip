@@ -80,6 +80,7 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
     p.G = a.page_tokens;
     p.Dk = a.d_boost;
     p.max_pages = a.max_pages;
+    p.flags = a.flags;
     p.pages_per_split = choose_pages_per_split(a);
     p.n_splits = (a.max_pages + p.pages_per_split - 1) / p.pages_per_split;
     p.sm_scale = a.sm_scale;

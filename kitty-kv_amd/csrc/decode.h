@@ -27,6 +27,7 @@ struct DecodeParams {
     int sink_cap, tail_cap;
     int B, Hq, Hkv, GQ, D, G, Dk;
     int max_pages, pages_per_split, n_splits;
+    int flags;
     float sm_scale;
     float *ws_o;  // [B][Hq][n_splits + 1][D] unnormalised partial outputs
     float *ws_ml; // [B][Hq][n_splits + 1][2] running max (log2 domain) and sum
@@ -35,6 +36,8 @@ struct DecodeParams {
 size_t generic_lds_bytes(int GQ, int D, int G, int Dk);
 int launch_generic(const DecodeParams &p, hipStream_t stream);
 int launch_splits(const DecodeParams &p, hipStream_t stream);
+bool mfma_path_supported(const DecodeParams &p);
+int launch_mfma(const DecodeParams &p, hipStream_t stream);
 int launch_merge(const DecodeParams &p, hipStream_t stream);
 
 } // namespace kitty

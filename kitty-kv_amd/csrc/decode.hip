@@ -328,8 +328,14 @@ int launch_generic(const DecodeParams &p, hipStream_t stream)
     return check_launch("decode_generic_kernel");
 }
 
-// Dispatch of the split phase: the generic kernel handles every shape.
-int launch_splits(const DecodeParams &p, hipStream_t stream) { return launch_generic(p, stream); }
+// Split phase: the MFMA kernel for the production shape, the generic kernel
+// for every other shape the reference accepts.
+int launch_splits(const DecodeParams &p, hipStream_t stream)
+{
+    if (mfma_path_supported(p))
+        return launch_mfma(p, stream);
+    return launch_generic(p, stream);
+}
 
 int launch_merge(const DecodeParams &p, hipStream_t stream)
 {

@@ -1,0 +1,552 @@
+// MFMA split-K paged decode for the production shape (D = G = 128,
+// D_boost <= 32, GQA group 4, 8 or 16) on gfx950.
+//
+// One wave (64 lanes) owns a work item (sequence b, KV head kh, range of
+// pages).  Per page it streams the 9.5-10 KB (page, head) record from HBM
+// into registers one page ahead, parks it in a 10 KB LDS stage, and:
+//
+//  QK   S[h][t] = sum_k A[h][k] * B[k][t] with v_mfma_f32_16x16x32_f16.
+//       B: 2-bit codes turned into fp16 by OR-ing them into the mantissa of
+//       1024 (0x6400 | c<<e gives 1024 + c*2^e exactly, 2 VALU ops per 4
+//       codes) after ds_read_b64_tr_b8 transposes the channel-major page in
+//       LDS so each lane holds 8 channels of one byte column (4 tokens).
+//       A: q * scale_k[d] * log2(e)/sqrt(D) / 2^e (fp16), heads on MFMA rows.
+//       The 1024 offsets and the zero points fold into one bias tile:
+//       C_init = -sum_k A[k] * (1024 + 2^e z_k), computed by 5 more MFMAs.
+//       High 2 bits of boosted channels are 16-32 extra reduction rows with
+//       A = 4 * q'[channel(rank)].
+//  softmax  online, base 2, one DPP row reduction per page.
+//  PV   O[h][d] = sum_t P'[h][t] * B[t][d], P' = p * s_t / 2^e (fp16) staged
+//       through a 1-2 KB LDS buffer; value codes get the same tr8 + OR
+//       treatment; the per-token zero points and 1024 offsets fold into a
+//       per-head bias subtracted from the accumulator at each page.
+//
+// Reduction index k of every MFMA follows the natural channel / token order
+// within a 32-wide step; the mantissa position of a code (bit 0 or bit 8 of a
+// half) is the per-k power 2^e in {1, 256}, compensated in A.
+#include "common.h"
+#include "decode.h"
+
+namespace kitty {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// LDS stage of one (page, head) record, byte offsets.
+constexpr int kKlo = 0;       // key low bits   (128 rows x 32 B), chunk-swizzled
+constexpr int kVal = 4096;    // value codes    (128 rows x 32 B), chunk-swizzled
+constexpr int kKhi = 8192;    // key high bits  (<= 32 rows x 32 B), chunk-swizzled
+constexpr int kMeta = 9216;   // key scale (256 B), key zero (256 B), value (scale, zero) (512 B)
+constexpr int kStage = 10240;
+
+// 16-byte chunk λ of a 128 x 32 B region lives at LDS slot λ; it holds row
+// λ/2, chunk (λ & 1) ^ ((row >> 3) & 1) of the page.  The XOR keeps the 32
+// rows read by one ds_read_b64_tr_b8 spread over all LDS banks.
+__device__ __forceinline__ int chunk_global_offset(int slot)
+{
+    const int row = slot >> 1;
+    return row * 32 + (((slot & 1) ^ ((row >> 3) & 1)) << 4);
+}
+
+__device__ __forceinline__ i32x2 tr8(const unsigned char *lds)
+{
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2 *)lds);
+}
+
+// Slot `a` (token 4j+a of a key byte, or channel 4j+a of a value byte) of the
+// 8 transposed bytes -> 8 fp16 MFMA inputs: rows (0,1) at 1024 + c, rows
+// (2,3) at 1024 + 256 c, then rows (4,5), (6,7) likewise.
+template <int A>
+__device__ __forceinline__ half8 codes_to_half8(i32x2 raw)
+{
+    const unsigned w0 = (unsigned)raw[0] >> (2 * A), w1 = (unsigned)raw[1] >> (2 * A);
+    u32x4 v;
+    v[0] = (w0 & 0x00030003u) | 0x64006400u;
+    v[1] = (w0 & 0x03000300u) | 0x64006400u;
+    v[2] = (w1 & 0x00030003u) | 0x64006400u;
+    v[3] = (w1 & 0x03000300u) | 0x64006400u;
+    return __builtin_bit_cast(half8, v);
+}
+
+__device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Reductions over the 16 lanes of a DPP row (one lane group = one head).
+__device__ __forceinline__ float row_max16(float v)
+{
+    v = fmaxf(v, dpp<0x128>(v));
+    v = fmaxf(v, dpp<0x124>(v));
+    v = fmaxf(v, dpp<0x122>(v));
+    v = fmaxf(v, dpp<0x121>(v));
+    return v;
+}
+
+__device__ __forceinline__ float row_sum16(float v)
+{
+    v += dpp<0x128>(v);
+    v += dpp<0x124>(v);
+    v += dpp<0x122>(v);
+    v += dpp<0x121>(v);
+    return v;
+}
+
+__device__ __forceinline__ unsigned pack_h2(float a, float b)
+{
+    half2v h;
+    h[0] = (_Float16)a;
+    h[1] = (_Float16)b;
+    return __builtin_bit_cast(unsigned, h);
+}
+
+__device__ __forceinline__ half2v as_h2(unsigned u) { return __builtin_bit_cast(half2v, u); }
+__device__ __forceinline__ unsigned as_u(half2v h) { return __builtin_bit_cast(unsigned, h); }
+
+// The (page, head) record in registers while it is in flight.
+struct PageRegs {
+    u32x4 klo[4], val[4], khi, meta;
+};
+
+struct PageSrc {
+    const unsigned char *klo, *val, *khi, *kmeta, *vmeta;
+};
+
+__device__ __forceinline__ PageSrc page_src(const DecodeParams &p, int64_t ph)
+{
+    PageSrc s;
+    s.klo = p.key_low + ph * 4096;
+    s.val = p.value + ph * 4096;
+    s.khi = p.key_high + ph * (int64_t)p.Dk * 32;
+    s.kmeta = (const unsigned char *)p.key_meta + ph * 512;
+    s.vmeta = (const unsigned char *)p.value_meta + ph * 512;
+    return s;
+}
+
+__device__ __forceinline__ void load_page(PageRegs &R, const PageSrc &s, int lane, int Dk)
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int off = chunk_global_offset(64 * j + lane);
+        R.klo[j] = __builtin_nontemporal_load((const u32x4 *)(s.klo + off));
+        R.val[j] = __builtin_nontemporal_load((const u32x4 *)(s.val + off));
+    }
+    if (lane < 2 * Dk)
+        R.khi = __builtin_nontemporal_load((const u32x4 *)(s.khi + chunk_global_offset(lane)));
+    const unsigned char *m = lane < 32 ? s.kmeta + 16 * lane : s.vmeta + 16 * (lane - 32);
+    R.meta = __builtin_nontemporal_load((const u32x4 *)m);
+}
+
+__device__ __forceinline__ void store_page(unsigned char *stage, const PageRegs &R, int lane, int Dk)
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        *(u32x4 *)(stage + kKlo + 1024 * j + 16 * lane) = R.klo[j];
+        *(u32x4 *)(stage + kVal + 1024 * j + 16 * lane) = R.val[j];
+    }
+    if (lane < 2 * Dk)
+        *(u32x4 *)(stage + kKhi + 16 * lane) = R.khi;
+    *(u32x4 *)(stage + kMeta + 16 * lane) = R.meta;
+}
+
+// FP16 sinks and tail of (b, kh), one wave, VALU.  Chunks of 64 tokens: lane
+// t scores token t for every head, lane l accumulates channels 2l, 2l+1.
+template <int GQ>
+__device__ void fp16_segments(const DecodeParams &p, int b, int kh, float *qs, float *pb, float *m_out,
+                              float *l_out, float (*O)[2])
+{
+    const int lane = threadIdx.x;
+    const float qscale = p.sm_scale * kLog2e;
+    for (int e = lane; e < GQ * 128; e += 64)
+        qs[e] = h2f(p.q[b * p.q_s_seq + (int64_t)(kh * GQ + e / 128) * p.q_s_head + (e & 127)]) * qscale;
+    float m[GQ], l[GQ];
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+        m[g] = -__builtin_inff();
+        l[g] = 0.0f;
+        O[g][0] = O[g][1] = 0.0f;
+    }
+    __syncthreads();
+    const int ns = min(max(0, p.sink_len[b]), p.sink_cap), nt = min(max(0, p.tail_len[b]), p.tail_cap);
+    for (int seg = 0; seg < 2; ++seg) {
+        const kitty_fp16_seg &K = seg == 0 ? p.sink_k : p.tail_k;
+        const kitty_fp16_seg &V = seg == 0 ? p.sink_v : p.tail_v;
+        const int n = seg == 0 ? ns : nt;
+        const uint16_t *kb = K.ptr + b * K.s_seq + kh * K.s_head;
+        const uint16_t *vb = V.ptr + b * V.s_seq + kh * V.s_head;
+        for (int c0 = 0; c0 < n; c0 += 64) {
+            const int cnt = min(64, n - c0);
+            float sc[GQ];
+#pragma unroll
+            for (int g = 0; g < GQ; ++g)
+                sc[g] = 0.0f;
+            if (lane < cnt) {
+                const uint16_t *row = kb + (int64_t)(c0 + lane) * K.s_tok;
+                for (int d0 = 0; d0 < 128; d0 += 8) {
+                    const u32x4 raw = *(const u32x4 *)(row + d0);
+                    float kv[8];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const half2v h = as_h2(raw[i]);
+                        kv[2 * i] = (float)h[0];
+                        kv[2 * i + 1] = (float)h[1];
+                    }
+#pragma unroll
+                    for (int g = 0; g < GQ; ++g)
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            sc[g] += qs[g * 128 + d0 + i] * kv[i];
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < GQ; ++g) {
+                float s = lane < cnt ? sc[g] : -__builtin_inff();
+                float mx = s;
+                for (int off = 32; off > 0; off >>= 1)
+                    mx = fmaxf(mx, __shfl_xor(mx, off));
+                const float mn = fmaxf(m[g], mx);
+                const float alpha = __builtin_amdgcn_exp2f(m[g] - mn);
+                const float pr = lane < cnt ? __builtin_amdgcn_exp2f(s - mn) : 0.0f;
+                float sum = pr;
+                for (int off = 32; off > 0; off >>= 1)
+                    sum += __shfl_xor(sum, off);
+                l[g] = l[g] * alpha + sum;
+                m[g] = mn;
+                O[g][0] *= alpha;
+                O[g][1] *= alpha;
+                pb[g * 64 + lane] = pr;
+            }
+            __syncthreads();
+            for (int t = 0; t < cnt; ++t) {
+                const unsigned v2 = *(const unsigned *)(vb + (int64_t)(c0 + t) * V.s_tok + 2 * lane);
+                const half2v h = as_h2(v2);
+                const float v0 = (float)h[0], v1 = (float)h[1];
+#pragma unroll
+                for (int g = 0; g < GQ; ++g) {
+                    const float w = pb[g * 64 + t];
+                    O[g][0] += w * v0;
+                    O[g][1] += w * v1;
+                }
+            }
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+        m_out[g] = m[g];
+        l_out[g] = l[g];
+    }
+}
+
+template <int GQ>
+__global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p)
+{
+    constexpr int HPL = GQ / 4;          // heads per lane group
+    constexpr int RSTEP = 4 / HPL;       // accumulator register of head j = j * RSTEP
+    constexpr int ROWS_PER_HEAD = 16 / GQ;
+    __shared__ __attribute__((aligned(16))) unsigned char stage[kStage];
+    __shared__ __attribute__((aligned(16))) _Float16 pbuf[(GQ + 1) * 128];  // + zero row
+    __shared__ int rank_chan[32];
+
+    const int lane = threadIdx.x, q = lane >> 4, r = lane & 15;
+    const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int NS = p.n_splits + 1;
+
+    if (split == p.n_splits) {
+        float m[GQ], l[GQ], O[GQ][2];
+        fp16_segments<GQ>(p, b, kh, (float *)stage, (float *)pbuf, m, l, O);
+        for (int g = 0; g < GQ; ++g) {
+            const int64_t row = ((int64_t)b * p.Hq + kh * GQ + g) * NS + split;
+            *(float2 *)(p.ws_o + row * 128 + 2 * lane) = make_float2(O[g][0], O[g][1]);
+            if (lane == 0) {
+                p.ws_ml[2 * row] = m[g];
+                p.ws_ml[2 * row + 1] = l[g];
+            }
+        }
+        return;
+    }
+
+    const int Dk = p.Dk;
+    const int np = p.num_pages[b];
+    bool poison = np < 0 || np > p.max_pages;
+    const int p0 = split * p.pages_per_split;
+    const int p1 = poison ? p0 : min(np, p0 + p.pages_per_split);
+
+    // rank -> channel map of this KV head (the inverse of boost_idx).
+    if (lane < 32)
+        rank_chan[lane] = 0;
+    __syncthreads();
+    for (int d = lane; d < 128; d += 64) {
+        const int bi = p.boost_idx[kh * 128 + d];
+        if (bi < Dk)
+            rank_chan[bi] = d;
+    }
+    for (int e = lane; e < 128; e += 64)
+        pbuf[GQ * 128 + e] = (_Float16)0.0f;
+    __syncthreads();
+
+    // Static halves of the QK A operand: q * sm_scale * log2(e) / 2^e for the
+    // lane's 8 channels of every K-step; zero on rows that carry no head.
+    const bool head_row = (r % ROWS_PER_HEAD) == 0;
+    const int hr = r / ROWS_PER_HEAD;  // head of MFMA row r
+    const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + (head_row ? hr : 0)) * p.q_s_head;
+    const float qscale = p.sm_scale * kLog2e;
+    u32x4 qv[4], qvh;
+    int hch[8];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = 32 * s + 8 * q + 2 * j;
+            const float inv = (j & 1) ? (1.0f / 256.0f) : 1.0f;
+            qv[s][j] = head_row ? pack_h2(h2f(qrow[c]) * qscale * inv, h2f(qrow[c + 1]) * qscale * inv) : 0u;
+        }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        hch[i] = rank_chan[8 * q + i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float inv = (j & 1) ? (4.0f / 256.0f) : 4.0f;
+        const int r0 = 8 * q + 2 * j;
+        const float a0 = (head_row && r0 < Dk) ? h2f(qrow[hch[2 * j]]) * qscale * inv : 0.0f;
+        const float a1 = (head_row && r0 + 1 < Dk) ? h2f(qrow[hch[2 * j + 1]]) * qscale * inv : 0.0f;
+        qvh[j] = pack_h2(a0, a1);
+    }
+    // B operand of the QK bias tile for the high rows: -1024 everywhere.
+    const half8 bw_hi = __builtin_bit_cast(half8, u32x4{0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u});
+    const half2v neg1024 = as_h2(0xE400E400u);
+    const half2v negs_lo = as_h2(0xBC00BC00u);   // -1
+    const half2v negs_hi = as_h2(0xDC00DC00u);   // -256
+    const half2v one1024 = as_h2(0x64006400u);
+    const half2v s256 = as_h2(0x5C005C00u);      // 256
+
+    // tr8 source address of this lane inside a 128 x 32 B region.
+    const int rho = ((r >> 1) & 4) | (((r >> 1) & 1) << 1) | (((r >> 1) >> 1) & 1);
+    const int tr_row = 8 * q + rho;
+    const int tr_base0 = 32 * tr_row + 16 * (0 ^ (q & 1)) + 8 * (r & 1);
+    const int tr_base1 = 32 * tr_row + 16 * (1 ^ (q & 1)) + 8 * (r & 1);
+
+    float m_run[HPL], l_run[HPL];
+    f32x4 O[2][4];
+#pragma unroll
+    for (int j = 0; j < HPL; ++j) {
+        m_run[j] = -__builtin_inff();
+        l_run[j] = 0.0f;
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+            O[cb][a] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    PageRegs R;
+    if (p0 < p1) {
+        const int32_t page = p.block_table[b * p.bt_stride + p0];
+        if (page < 0 || page >= p.num_pool_pages)
+            poison = true;
+        else {
+            load_page(R, page_src(p, (int64_t)page * p.Hkv + kh), lane, Dk);
+            store_page(stage, R, lane, Dk);
+        }
+    }
+    for (int pi = p0; pi < p1 && !poison; ++pi) {
+        bool have_next = false;
+        if (pi + 1 < p1) {
+            const int32_t page = p.block_table[b * p.bt_stride + pi + 1];
+            if (page < 0 || page >= p.num_pool_pages)
+                poison = true;  // finish this page, then stop
+            else {
+                load_page(R, page_src(p, (int64_t)page * p.Hkv + kh), lane, Dk);
+                have_next = true;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this page's stores are in LDS
+
+        // ---------------- QK A operands and bias tile
+        half8 A[4], Ahi;
+        f32x4 bias = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const u32x4 ks = *(const u32x4 *)(stage + kMeta + 2 * (32 * s + 8 * q));
+            const u32x4 kz = *(const u32x4 *)(stage + kMeta + 256 + 2 * (32 * s + 8 * q));
+            u32x4 av, bw;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                av[j] = as_u(as_h2(qv[s][j]) * as_h2(ks[j]));
+                bw[j] = as_u(__builtin_elementwise_fma(as_h2(kz[j]), (j & 1) ? negs_hi : negs_lo, neg1024));
+            }
+            A[s] = __builtin_bit_cast(half8, av);
+            bias = mfma(A[s], __builtin_bit_cast(half8, bw), bias);
+        }
+        if (Dk > 0) {
+            u32x4 ksh, av;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                half2v h;
+                h[0] = *(const _Float16 *)(stage + kMeta + 2 * hch[2 * j]);
+                h[1] = *(const _Float16 *)(stage + kMeta + 2 * hch[2 * j + 1]);
+                ksh[j] = as_u(h);
+                av[j] = as_u(as_h2(qvh[j]) * h);
+            }
+            Ahi = __builtin_bit_cast(half8, av);
+            bias = mfma(Ahi, bw_hi, bias);
+        }
+
+        // ---------------- QK token tiles: S[cb][a] covers tokens 64cb + 4r + a
+        f32x4 S[2][4];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+                S[cb][a] = bias;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const i32x2 raw = tr8(stage + kKlo + 1024 * s + (cb ? tr_base1 : tr_base0));
+                S[cb][0] = mfma(A[s], codes_to_half8<0>(raw), S[cb][0]);
+                S[cb][1] = mfma(A[s], codes_to_half8<1>(raw), S[cb][1]);
+                S[cb][2] = mfma(A[s], codes_to_half8<2>(raw), S[cb][2]);
+                S[cb][3] = mfma(A[s], codes_to_half8<3>(raw), S[cb][3]);
+            }
+        if (Dk > 0) {
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const i32x2 raw = tr8(stage + kKhi + (cb ? tr_base1 : tr_base0));
+                S[cb][0] = mfma(Ahi, codes_to_half8<0>(raw), S[cb][0]);
+                S[cb][1] = mfma(Ahi, codes_to_half8<1>(raw), S[cb][1]);
+                S[cb][2] = mfma(Ahi, codes_to_half8<2>(raw), S[cb][2]);
+                S[cb][3] = mfma(Ahi, codes_to_half8<3>(raw), S[cb][3]);
+            }
+        }
+
+        // ---------------- online softmax and P' (fp16) with the PV bias
+        const u32x4 vm0 = *(const u32x4 *)(stage + kMeta + 512 + 4 * (4 * r));
+        const u32x4 vm1 = *(const u32x4 *)(stage + kMeta + 512 + 4 * (64 + 4 * r));
+        float alpha[HPL], vbias[HPL];
+#pragma unroll
+        for (int j = 0; j < HPL; ++j) {
+            const int ri = j * RSTEP;
+            float mx = S[0][0][ri];
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+                    mx = fmaxf(mx, S[cb][a][ri]);
+            mx = row_max16(mx);
+            const float mn = fmaxf(m_run[j], mx);
+            alpha[j] = __builtin_amdgcn_exp2f(m_run[j] - mn);
+            m_run[j] = mn;
+            float lsum = 0.0f, lsum256 = 0.0f, bsum = 0.0f;
+            const int h = q * HPL + j;
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const u32x4 vm = cb ? vm1 : vm0;
+                const float p0v = __builtin_amdgcn_exp2f(S[cb][0][ri] - mn);
+                const float p1v = __builtin_amdgcn_exp2f(S[cb][1][ri] - mn);
+                const float p2v = __builtin_amdgcn_exp2f(S[cb][2][ri] - mn - 8.0f);  // p / 256
+                const float p3v = __builtin_amdgcn_exp2f(S[cb][3][ri] - mn - 8.0f);
+                lsum += p0v + p1v;
+                lsum256 += p2v + p3v;
+                // (scale, zero) pairs of tokens 64cb + 4r + {0..3}
+                const half2v sv01 = as_h2(__builtin_amdgcn_perm(vm[1], vm[0], 0x05040100u));
+                const half2v zv01 = as_h2(__builtin_amdgcn_perm(vm[1], vm[0], 0x07060302u));
+                const half2v sv23 = as_h2(__builtin_amdgcn_perm(vm[3], vm[2], 0x05040100u));
+                const half2v zv23 = as_h2(__builtin_amdgcn_perm(vm[3], vm[2], 0x07060302u));
+                const half2v a01 = as_h2(pack_h2(p0v, p1v)) * sv01;
+                const half2v a23 = as_h2(pack_h2(p2v, p3v)) * sv23;
+                const half2v w01 = zv01 + one1024;
+                const half2v w23 = __builtin_elementwise_fma(zv23, s256, one1024);
+                bsum = __builtin_amdgcn_fdot2(a01, w01, bsum, false);
+                bsum = __builtin_amdgcn_fdot2(a23, w23, bsum, false);
+                *(uint2 *)(pbuf + h * 128 + 64 * cb + 4 * r) = make_uint2(as_u(a01), as_u(a23));
+            }
+            l_run[j] = l_run[j] * alpha[j] + lsum + 256.0f * lsum256;
+            vbias[j] = row_sum16(bsum);
+        }
+
+        // ---------------- PV: O = O * alpha - bias + P' V
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int j = 0; j < HPL; ++j)
+                    O[cb][a][j * RSTEP] = O[cb][a][j * RSTEP] * alpha[j] - vbias[j];
+        const int prow = head_row ? hr : GQ;  // the zero row for MFMA rows without a head
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const half8 Ap = *(const half8 *)(pbuf + prow * 128 + 32 * s + 8 * q);
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const i32x2 raw = tr8(stage + kVal + 1024 * s + (cb ? tr_base1 : tr_base0));
+                O[cb][0] = mfma(Ap, codes_to_half8<0>(raw), O[cb][0]);
+                O[cb][1] = mfma(Ap, codes_to_half8<1>(raw), O[cb][1]);
+                O[cb][2] = mfma(Ap, codes_to_half8<2>(raw), O[cb][2]);
+                O[cb][3] = mfma(Ap, codes_to_half8<3>(raw), O[cb][3]);
+            }
+        }
+        if (have_next) {
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // every LDS read of this page has returned
+            store_page(stage, R, lane, Dk);
+        }
+    }
+
+    // ---------------------------------------------------- write partial
+#pragma unroll
+    for (int j = 0; j < HPL; ++j) {
+        const float l = row_sum16(l_run[j]);
+        const int h = q * HPL + j;
+        const int64_t row = ((int64_t)b * p.Hq + kh * GQ + h) * NS + split;
+        float *o = p.ws_o + row * 128;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            float4 v = make_float4(O[cb][0][j * RSTEP], O[cb][1][j * RSTEP], O[cb][2][j * RSTEP],
+                                   O[cb][3][j * RSTEP]);
+            if (poison)
+                v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+            *(float4 *)(o + 64 * cb + 4 * r) = v;
+        }
+        if (r == 0) {
+            p.ws_ml[2 * row] = poison ? __builtin_nanf("") : m_run[j];
+            p.ws_ml[2 * row + 1] = l;
+        }
+    }
+}
+
+static bool seg_aligned(const kitty_fp16_seg &s)
+{
+    return ((uintptr_t)s.ptr & 15) == 0 && s.s_seq % 8 == 0 && s.s_head % 8 == 0 && s.s_tok % 8 == 0;
+}
+
+bool mfma_path_supported(const DecodeParams &p)
+{
+    return p.D == 128 && p.G == 128 && p.Dk >= 0 && p.Dk <= 32 && (p.GQ == 4 || p.GQ == 8 || p.GQ == 16) &&
+           (p.flags & KITTY_DECODE_UNIQUE_BOOST_ROWS) && seg_aligned(p.sink_k) && seg_aligned(p.sink_v) &&
+           seg_aligned(p.tail_k) && seg_aligned(p.tail_v) && ((uintptr_t)p.key_low & 15) == 0 &&
+           ((uintptr_t)p.key_high & 15) == 0 && ((uintptr_t)p.key_meta & 15) == 0 &&
+           ((uintptr_t)p.value & 15) == 0 && ((uintptr_t)p.value_meta & 15) == 0;
+}
+
+int launch_mfma(const DecodeParams &p, hipStream_t stream)
+{
+    dim3 grid(p.n_splits + 1, p.Hkv, p.B);
+    switch (p.GQ) {
+    case 4: hipLaunchKernelGGL(decode_mfma_kernel<4>, grid, dim3(64), 0, stream, p); break;
+    case 8: hipLaunchKernelGGL(decode_mfma_kernel<8>, grid, dim3(64), 0, stream, p); break;
+    case 16: hipLaunchKernelGGL(decode_mfma_kernel<16>, grid, dim3(64), 0, stream, p); break;
+    default: return fail(KITTY_E_UNSUPPORTED, "MFMA decode needs a GQA group of 4, 8 or 16");
+    }
+    return check_launch("decode_mfma_kernel");
+}
+
+} // namespace kitty

@@ -24,6 +24,7 @@ KITTY_E_HIP = -2
 KITTY_E_UNSUPPORTED = -3
 KITTY_E_EXHAUSTED = -4
 KITTY_E_NOT_FOUND = -5
+KITTY_DECODE_UNIQUE_BOOST_ROWS = 1
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -72,7 +73,7 @@ class DecodeArgs(ctypes.Structure):
         ("sink_len", _vp), ("tail_len", _vp), ("sink_capacity", _i32), ("tail_capacity", _i32),
         ("batch", _i32), ("num_q_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
         ("page_tokens", _i32), ("d_boost", _i32), ("max_pages", _i32), ("pages_per_split", _i32),
-        ("sm_scale", ctypes.c_float),
+        ("flags", _i32), ("sm_scale", ctypes.c_float),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
     ]
 

@@ -112,6 +112,17 @@ def quantize_into_pools(store: _hip.PageStore, key: Optional[torch.Tensor], valu
 
 # --------------------------------------------------------------- decode
 
+def boost_rows_unique(boost_idx: torch.Tensor, d_boost: int) -> bool:
+    """True when no rank below d_boost repeats within a boost_idx row (one
+    small device-to-host copy); the MFMA decode path relies on it."""
+    bi = boost_idx.detach().to("cpu", torch.int64).reshape(-1, boost_idx.shape[-1])
+    for row in bi:
+        ranks = row[row < d_boost]
+        if ranks.numel() != torch.unique(ranks).numel():
+            return False
+    return True
+
+
 class DecodePlan:
     """Validated, pre-built arguments of one batched paged-decode call.
 
@@ -141,7 +152,8 @@ class DecodePlan:
         _check_fp16("q", q)
         for name, t in (("sink_k", sink_k), ("sink_v", sink_v), ("tail_k", tail_k), ("tail_v", tail_v)):
             _check_fp16(name, t)
-            _need(t.dim() == 4 and t.shape[0] == B and t.shape[1] == Hkv and t.shape[3] == D and t.stride(3) == 1,
+            _need(t.dim() == 4 and t.shape[0] == B and t.shape[1] == Hkv and t.shape[3] == D
+                  and (t.shape[2] == 0 or t.stride(3) == 1),
                   f"{name} must be (B, Hkv, n, D) with contiguous channels")
         _need(q.stride(2) == 1, "q channels must be contiguous")
         _need(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == B
@@ -176,6 +188,7 @@ class DecodePlan:
         a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, D
         a.page_tokens, a.d_boost = G4 * 4, key_boost.shape[2]
         a.max_pages, a.pages_per_split = int(max_pages), int(pages_per_split)
+        a.flags = _hip.KITTY_DECODE_UNIQUE_BOOST_ROWS if boost_rows_unique(boost_idx, key_boost.shape[2]) else 0
         a.sm_scale = float(1.0 / math.sqrt(D) if sm_scale is None else sm_scale)
         self._L = _hip.load()
         need = ctypes.c_size_t(0)
