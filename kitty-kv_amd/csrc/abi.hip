@@ -12,21 +12,33 @@ static thread_local std::string g_last_error;
 void set_error(const std::string &msg) { g_last_error = msg; }
 const char *get_error() { return g_last_error.c_str(); }
 
-// Split size: enough (b, kh, split) work items to cover the 256 CUs several
-// times over, but at least 4 pages per split so partials stay small.
+// Waves of the MFMA decode kernel resident on the current device at once:
+// 8 per CU (20 KB of LDS and 256 registers each), 2048 on an MI355X.
+static int64_t resident_waves()
+{
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    return 8 * (int64_t)cus;
+}
+
+// Split size.  Every (b, kh) pair gets n_splits page splits plus one FP16
+// split; when the batch allows it, the total is kept within one resident
+// round of waves, because a handful of waves left over for a second round
+// doubles the kernel time.  Splits hold 4..kMaxPagesPerSplit pages (one page
+// id per lane of a wave).
 static int choose_pages_per_split(const kitty_decode_args &a)
 {
     if (a.pages_per_split > 0)
-        return a.pages_per_split;
+        return a.pages_per_split > kMaxPagesPerSplit ? kMaxPagesPerSplit : a.pages_per_split;
     const int64_t pairs = (int64_t)a.batch * a.num_kv_heads;
-    const int64_t target_items = 2048;
-    int64_t splits = (target_items + pairs - 1) / (pairs > 0 ? pairs : 1);
-    if (splits < 1)
-        splits = 1;
+    const int64_t per_pair = resident_waves() / (pairs > 0 ? pairs : 1);
+    const int64_t splits = per_pair >= 2 ? per_pair - 1 : 1;
     int64_t pps = (a.max_pages + splits - 1) / splits;
     if (pps < 4)
         pps = 4;
-    return (int)pps;
+    return (int)(pps > kMaxPagesPerSplit ? kMaxPagesPerSplit : pps);
 }
 
 static int build_params(const kitty_decode_args *args, DecodeParams &p)

@@ -5,6 +5,7 @@
 namespace kitty {
 
 constexpr int kChunkMax = 256; // tokens per softmax chunk in the generic path (>= G)
+constexpr int kMaxPagesPerSplit = 64;
 
 struct DecodeParams {
     const uint16_t *q;

@@ -263,37 +263,63 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
     }
 }
 
-// Combine the n_splits + 1 partials of (b, qh) and write fp16 output.
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p)
+// Combine the n_splits + 1 partials of (b, qh) and write the fp16 output.
+// One wave per (b, qh); each lane owns channels lane and lane + 64 (D <= 128
+// per pass).  Splits are taken 16 at a time with every load of a batch
+// issued together, and merged with a running maximum, so a batch costs one
+// memory round trip.
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
 {
+    constexpr int kBatch = 16;
+    const int lane = threadIdx.x;
     const int bq = blockIdx.x;
     const int b = bq / p.Hq, qh = bq - b * p.Hq;
     const int NS = p.n_splits + 1;
     const int64_t row0 = (int64_t)bq * NS;
-    float M = -__builtin_inff();
-    bool nan = false;
-    for (int s2 = 0; s2 < NS; ++s2) {
-        const float m = p.ws_ml[2 * (row0 + s2)];
-        nan |= m != m;
-        M = fmaxf(M, m);
-    }
-    float L = 0.0f;
-    for (int s2 = 0; s2 < NS; ++s2) {
-        const float m = p.ws_ml[2 * (row0 + s2)];
-        if (m != -__builtin_inff())
-            L += p.ws_ml[2 * (row0 + s2) + 1] * exp2f(m - M);
-    }
-    for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
-        float acc = 0.0f;
-        for (int s2 = 0; s2 < NS; ++s2) {
-            const float m = p.ws_ml[2 * (row0 + s2)];
-            if (m != -__builtin_inff())
-                acc += p.ws_o[(row0 + s2) * p.D + d] * exp2f(m - M);
+    const float ninf = -__builtin_inff();
+    for (int d0 = 0; d0 < p.D; d0 += 128) {
+        const int da = d0 + lane, db = d0 + 64 + lane;
+        float M = ninf, L = 0.0f, acc_a = 0.0f, acc_b = 0.0f;
+        bool nan = false;
+        for (int s0 = 0; s0 < NS; s0 += kBatch) {
+            float m[kBatch], l[kBatch], oa[kBatch], ob[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const bool ok = s0 + u < NS;
+                const int64_t row = row0 + (ok ? s0 + u : 0);
+                m[u] = ok ? p.ws_ml[2 * row] : ninf;
+                l[u] = ok ? p.ws_ml[2 * row + 1] : 0.0f;
+                oa[u] = ok && da < p.D ? p.ws_o[row * p.D + da] : 0.0f;
+                ob[u] = ok && db < p.D ? p.ws_o[row * p.D + db] : 0.0f;
+            }
+            float bm = ninf;
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                nan |= m[u] != m[u];
+                bm = fmaxf(bm, m[u]);
+            }
+            const float Mn = fmaxf(M, bm);
+            if (Mn == ninf)
+                continue;  // nothing attended yet
+            const float r = exp2f(M - Mn);
+            L *= r;
+            acc_a *= r;
+            acc_b *= r;
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const float w = m[u] != ninf ? exp2f(m[u] - Mn) : 0.0f;
+                L += l[u] * w;
+                acc_a += oa[u] * w;
+                acc_b += ob[u] * w;
+            }
+            M = Mn;
         }
-        float o = L > 0.0f ? acc / L : 0.0f; // no tokens -> zeros (attention.py:180-182)
-        if (nan)
-            o = __builtin_nanf("");
-        p.out[b * p.out_s_seq + qh * p.out_s_head + d] = f2h(o);
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;  // no tokens -> zeros (attention.py:180-182)
+        uint16_t *o = p.out + b * p.out_s_seq + qh * p.out_s_head;
+        if (da < p.D)
+            o[da] = f2h(nan ? __builtin_nanf("") : acc_a * inv);
+        if (db < p.D)
+            o[db] = f2h(nan ? __builtin_nanf("") : acc_b * inv);
     }
 }
 
@@ -339,7 +365,7 @@ int launch_splits(const DecodeParams &p, hipStream_t stream)
 
 int launch_merge(const DecodeParams &p, hipStream_t stream)
 {
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(p.B * p.Hq), dim3(128), 0, stream, p);
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(p.B * p.Hq), dim3(64), 0, stream, p);
     return check_launch("decode_merge_kernel");
 }
 

@@ -59,15 +59,28 @@ __device__ __forceinline__ i32x2 tr8(const unsigned char *lds)
 // Slot `a` (token 4j+a of a key byte, or channel 4j+a of a value byte) of the
 // 8 transposed bytes -> 8 fp16 MFMA inputs: rows (0,1) at 1024 + c, rows
 // (2,3) at 1024 + 256 c, then rows (4,5), (6,7) likewise.
+// The three masks live in VGPRs (see CodeMasks) so each half pair is one
+// v_and_or_b32; gfx9 VOP3 cannot encode two literal operands.
+struct CodeMasks {
+    unsigned lo, hi, one;  // 0x00030003, 0x03000300, 0x64006400
+};
+
+__device__ __forceinline__ CodeMasks code_masks()
+{
+    CodeMasks m{0x00030003u, 0x03000300u, 0x64006400u};
+    asm volatile("" : "+v"(m.lo), "+v"(m.hi), "+v"(m.one));
+    return m;
+}
+
 template <int A>
-__device__ __forceinline__ half8 codes_to_half8(i32x2 raw)
+__device__ __forceinline__ half8 codes_to_half8(i32x2 raw, const CodeMasks &m)
 {
     const unsigned w0 = (unsigned)raw[0] >> (2 * A), w1 = (unsigned)raw[1] >> (2 * A);
     u32x4 v;
-    v[0] = (w0 & 0x00030003u) | 0x64006400u;
-    v[1] = (w0 & 0x03000300u) | 0x64006400u;
-    v[2] = (w1 & 0x00030003u) | 0x64006400u;
-    v[3] = (w1 & 0x03000300u) | 0x64006400u;
+    v[0] = (w0 & m.lo) | m.one;
+    v[1] = (w0 & m.hi) | m.one;
+    v[2] = (w1 & m.lo) | m.one;
+    v[3] = (w1 & m.hi) | m.one;
     return __builtin_bit_cast(half8, v);
 }
 
@@ -112,11 +125,6 @@ __device__ __forceinline__ unsigned pack_h2(float a, float b)
 __device__ __forceinline__ half2v as_h2(unsigned u) { return __builtin_bit_cast(half2v, u); }
 __device__ __forceinline__ unsigned as_u(half2v h) { return __builtin_bit_cast(unsigned, h); }
 
-// The (page, head) record in registers while it is in flight.
-struct PageRegs {
-    u32x4 klo[4], val[4], khi, meta;
-};
-
 struct PageSrc {
     const unsigned char *klo, *val, *khi, *kmeta, *vmeta;
 };
@@ -132,34 +140,45 @@ __device__ __forceinline__ PageSrc page_src(const DecodeParams &p, int64_t ph)
     return s;
 }
 
-__device__ __forceinline__ void load_page(PageRegs &R, const PageSrc &s, int lane, int Dk)
+// global_load_lds_dwordx4: lane l's 16 bytes land at lds_base + 16 l.  The
+// pages are streamed once, so the loads carry the non-temporal hint.
+constexpr int kLoadAux = 2;
+__device__ __forceinline__ void gll16(const unsigned char *src, unsigned char *lds_base)
+{
+    __builtin_amdgcn_global_load_lds((const void *)src, (__attribute__((address_space(3))) void *)lds_base, 16, 0,
+                                     kLoadAux);
+}
+
+// Ten direct-to-LDS loads of one (page, head) record; lane l fetches the
+// chunk that belongs in LDS slot l (chunk_global_offset), which applies the
+// bank swizzle without extra instructions.  Lanes past 2*Dk re-read a valid
+// metadata chunk into unused K-high slots, so every page issues exactly
+// kLoadsPerPage loads.
+constexpr int kLoadsPerPage = 10;
+
+__device__ __forceinline__ void issue_page(unsigned char *st, const PageSrc &s, int lane, int Dk)
 {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int off = chunk_global_offset(64 * j + lane);
-        R.klo[j] = __builtin_nontemporal_load((const u32x4 *)(s.klo + off));
-        R.val[j] = __builtin_nontemporal_load((const u32x4 *)(s.val + off));
+        gll16(s.klo + off, st + kKlo + 1024 * j);
+        gll16(s.val + off, st + kVal + 1024 * j);
     }
-    if (lane < 2 * Dk)
-        R.khi = __builtin_nontemporal_load((const u32x4 *)(s.khi + chunk_global_offset(lane)));
-    const unsigned char *m = lane < 32 ? s.kmeta + 16 * lane : s.vmeta + 16 * (lane - 32);
-    R.meta = __builtin_nontemporal_load((const u32x4 *)m);
+    gll16(lane < 2 * Dk ? s.khi + chunk_global_offset(lane) : s.kmeta, st + kKhi);
+    gll16(lane < 32 ? s.kmeta + 16 * lane : s.vmeta + 16 * (lane - 32), st + kMeta);
 }
 
-__device__ __forceinline__ void store_page(unsigned char *stage, const PageRegs &R, int lane, int Dk)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
 {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        *(u32x4 *)(stage + kKlo + 1024 * j + 16 * lane) = R.klo[j];
-        *(u32x4 *)(stage + kVal + 1024 * j + 16 * lane) = R.val[j];
-    }
-    if (lane < 2 * Dk)
-        *(u32x4 *)(stage + kKhi + 16 * lane) = R.khi;
-    *(u32x4 *)(stage + kMeta + 16 * lane) = R.meta;
+    // s_waitcnt vmcnt(N) expcnt(7) lgkmcnt(15)
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 // FP16 sinks and tail of (b, kh), one wave, VALU.  Chunks of 64 tokens: lane
-// t scores token t for every head, lane l accumulates channels 2l, 2l+1.
+// t scores token t for every head (its K row read as 16 independent 16-byte
+// loads), then lane l accumulates channels 2l, 2l+1 over the chunk, reading
+// 16 value rows per batch of independent loads.
 template <int GQ>
 __device__ void fp16_segments(const DecodeParams &p, int b, int kh, float *qs, float *pb, float *m_out,
                               float *l_out, float (*O)[2])
@@ -185,31 +204,38 @@ __device__ void fp16_segments(const DecodeParams &p, int b, int kh, float *qs, f
         const uint16_t *vb = V.ptr + b * V.s_seq + kh * V.s_head;
         for (int c0 = 0; c0 < n; c0 += 64) {
             const int cnt = min(64, n - c0);
+            const uint16_t *row = kb + (int64_t)(c0 + min(lane, cnt - 1)) * K.s_tok;
             float sc[GQ];
 #pragma unroll
             for (int g = 0; g < GQ; ++g)
                 sc[g] = 0.0f;
-            if (lane < cnt) {
-                const uint16_t *row = kb + (int64_t)(c0 + lane) * K.s_tok;
-                for (int d0 = 0; d0 < 128; d0 += 8) {
-                    const u32x4 raw = *(const u32x4 *)(row + d0);
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                u32x4 kr[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    kr[i] = *(const u32x4 *)(row + 64 * hf + 8 * i);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
                     float kv[8];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const half2v h = as_h2(raw[i]);
-                        kv[2 * i] = (float)h[0];
-                        kv[2 * i + 1] = (float)h[1];
+                    for (int e = 0; e < 4; ++e) {
+                        const half2v h = as_h2(kr[i][e]);
+                        kv[2 * e] = (float)h[0];
+                        kv[2 * e + 1] = (float)h[1];
                     }
 #pragma unroll
-                    for (int g = 0; g < GQ; ++g)
-#pragma unroll
-                        for (int i = 0; i < 8; ++i)
-                            sc[g] += qs[g * 128 + d0 + i] * kv[i];
+                    for (int g = 0; g < GQ; ++g) {
+                        const float4 q0 = *(const float4 *)(qs + g * 128 + 64 * hf + 8 * i);
+                        const float4 q1 = *(const float4 *)(qs + g * 128 + 64 * hf + 8 * i + 4);
+                        sc[g] += q0.x * kv[0] + q0.y * kv[1] + q0.z * kv[2] + q0.w * kv[3] + q1.x * kv[4] +
+                                 q1.y * kv[5] + q1.z * kv[6] + q1.w * kv[7];
+                    }
                 }
             }
 #pragma unroll
             for (int g = 0; g < GQ; ++g) {
-                float s = lane < cnt ? sc[g] : -__builtin_inff();
+                const float s = lane < cnt ? sc[g] : -__builtin_inff();
                 float mx = s;
                 for (int off = 32; off > 0; off >>= 1)
                     mx = fmaxf(mx, __shfl_xor(mx, off));
@@ -226,15 +252,21 @@ __device__ void fp16_segments(const DecodeParams &p, int b, int kh, float *qs, f
                 pb[g * 64 + lane] = pr;
             }
             __syncthreads();
-            for (int t = 0; t < cnt; ++t) {
-                const unsigned v2 = *(const unsigned *)(vb + (int64_t)(c0 + t) * V.s_tok + 2 * lane);
-                const half2v h = as_h2(v2);
-                const float v0 = (float)h[0], v1 = (float)h[1];
+            for (int t0 = 0; t0 < cnt; t0 += 16) {
+                unsigned vv[16];
 #pragma unroll
-                for (int g = 0; g < GQ; ++g) {
-                    const float w = pb[g * 64 + t];
-                    O[g][0] += w * v0;
-                    O[g][1] += w * v1;
+                for (int j = 0; j < 16; ++j)
+                    vv[j] = *(const unsigned *)(vb + (int64_t)(c0 + min(t0 + j, cnt - 1)) * V.s_tok + 2 * lane);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const half2v h = as_h2(vv[j]);
+                    const float v0 = (float)h[0], v1 = (float)h[1];
+#pragma unroll
+                    for (int g = 0; g < GQ; ++g) {
+                        const float w = t0 + j < cnt ? pb[g * 64 + t0 + j] : 0.0f;
+                        O[g][0] += w * v0;
+                        O[g][1] += w * v1;
+                    }
                 }
             }
             __syncthreads();
@@ -247,15 +279,214 @@ __device__ void fp16_segments(const DecodeParams &p, int b, int kh, float *qs, f
     }
 }
 
+// Running state of one wave across its pages.
 template <int GQ>
-__global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p)
+struct WaveState {
+    static constexpr int HPL = GQ / 4;      // heads per lane group
+    u32x4 qv[4], qvh;                        // static halves of the QK A operand
+    int hch[8];                              // channel of high-bit row 8q + i
+    int tr_base0, tr_base1;                  // tr8 source offsets (byte columns 0-15 / 16-31)
+    int prow;                                // head row whose P' this lane reads for PV
+    float m_run[HPL], l_run[HPL];
+    f32x4 O[2][4];
+};
+
+// One (page, head) record in LDS stage `st` -> QK, online softmax, PV.
+template <int GQ>
+__device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st, int lane, int Dk)
 {
-    constexpr int HPL = GQ / 4;          // heads per lane group
-    constexpr int RSTEP = 4 / HPL;       // accumulator register of head j = j * RSTEP
+    constexpr int HPL = GQ / 4;
+    constexpr int RSTEP = 4 / HPL;  // accumulator register of head slot j = j * RSTEP
+    const int q = lane >> 4, r = lane & 15;
+    const half8 bw_hi = __builtin_bit_cast(half8, u32x4{0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u});
+    const half2v neg1024 = as_h2(0xE400E400u);
+    const half2v negs_lo = as_h2(0xBC00BC00u);   // -1
+    const half2v negs_hi = as_h2(0xDC00DC00u);   // -256
+    const half2v one1024 = as_h2(0x64006400u);
+    const half2v s256 = as_h2(0x5C005C00u);      // 256
+
+    const CodeMasks cm = code_masks();
+
+    // ---------------- operands from LDS, issued together
+    u32x4 ks[4], kz[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        ks[s] = *(const u32x4 *)(st + kMeta + 2 * (32 * s + 8 * q));
+        kz[s] = *(const u32x4 *)(st + kMeta + 256 + 2 * (32 * s + 8 * q));
+    }
+    i32x2 kraw[4][2], hraw[2];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        kraw[s][0] = tr8(st + kKlo + 1024 * s + W.tr_base0);
+        kraw[s][1] = tr8(st + kKlo + 1024 * s + W.tr_base1);
+    }
+    _Float16 ksh[8];
+    if (Dk > 0) {
+        hraw[0] = tr8(st + kKhi + W.tr_base0);
+        hraw[1] = tr8(st + kKhi + W.tr_base1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            ksh[i] = *(const _Float16 *)(st + kMeta + 2 * W.hch[i]);
+    }
+
+    // ---------------- QK A operands and bias tile
+    half8 A[4], Ahi;
+    f32x4 bias = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        u32x4 av, bw;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            av[j] = as_u(as_h2(W.qv[s][j]) * as_h2(ks[s][j]));
+            bw[j] = as_u(__builtin_elementwise_fma(as_h2(kz[s][j]), (j & 1) ? negs_hi : negs_lo, neg1024));
+        }
+        A[s] = __builtin_bit_cast(half8, av);
+        bias = mfma(A[s], __builtin_bit_cast(half8, bw), bias);
+    }
+    if (Dk > 0) {
+        u32x4 av;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            half2v h;
+            h[0] = ksh[2 * j];
+            h[1] = ksh[2 * j + 1];
+            av[j] = as_u(as_h2(W.qvh[j]) * h);
+        }
+        Ahi = __builtin_bit_cast(half8, av);
+        bias = mfma(Ahi, bw_hi, bias);
+    }
+
+    // ---------------- QK token tiles: S[cb][a] covers tokens 64cb + 4r + a
+    f32x4 S[2][4];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+            S[cb][a] = bias;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            S[cb][0] = mfma(A[s], codes_to_half8<0>(kraw[s][cb], cm), S[cb][0]);
+            S[cb][1] = mfma(A[s], codes_to_half8<1>(kraw[s][cb], cm), S[cb][1]);
+            S[cb][2] = mfma(A[s], codes_to_half8<2>(kraw[s][cb], cm), S[cb][2]);
+            S[cb][3] = mfma(A[s], codes_to_half8<3>(kraw[s][cb], cm), S[cb][3]);
+        }
+    if (Dk > 0) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            S[cb][0] = mfma(Ahi, codes_to_half8<0>(hraw[cb], cm), S[cb][0]);
+            S[cb][1] = mfma(Ahi, codes_to_half8<1>(hraw[cb], cm), S[cb][1]);
+            S[cb][2] = mfma(Ahi, codes_to_half8<2>(hraw[cb], cm), S[cb][2]);
+            S[cb][3] = mfma(Ahi, codes_to_half8<3>(hraw[cb], cm), S[cb][3]);
+        }
+    }
+
+    // value codes for PV, issued before the softmax so they arrive meanwhile
+    i32x2 vraw[4][2];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        vraw[s][0] = tr8(st + kVal + 1024 * s + W.tr_base0);
+        vraw[s][1] = tr8(st + kVal + 1024 * s + W.tr_base1);
+    }
+
+    // ---------------- online softmax and P' (fp16) with the PV bias.
+    // P' goes to the key-low region of this stage, whose codes are consumed.
+    _Float16 *pbuf = (_Float16 *)(st + kKlo);
+    const u32x4 vm0 = *(const u32x4 *)(st + kMeta + 512 + 4 * (4 * r));
+    const u32x4 vm1 = *(const u32x4 *)(st + kMeta + 512 + 4 * (64 + 4 * r));
+    float alpha[HPL], vbias[HPL];
+#pragma unroll
+    for (int j = 0; j < HPL; ++j) {
+        const int ri = j * RSTEP;
+        float mx = S[0][0][ri];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+                mx = fmaxf(mx, S[cb][a][ri]);
+        mx = row_max16(mx);
+        const float mn = fmaxf(W.m_run[j], mx);
+        alpha[j] = __builtin_amdgcn_exp2f(W.m_run[j] - mn);
+        W.m_run[j] = mn;
+        float lsum = 0.0f, lsum256 = 0.0f, bsum = 0.0f;
+        const int h = q * HPL + j;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            const u32x4 vm = cb ? vm1 : vm0;
+            const float p0v = __builtin_amdgcn_exp2f(S[cb][0][ri] - mn);
+            const float p1v = __builtin_amdgcn_exp2f(S[cb][1][ri] - mn);
+            const float p2v = __builtin_amdgcn_exp2f(S[cb][2][ri] - mn - 8.0f);  // p / 256
+            const float p3v = __builtin_amdgcn_exp2f(S[cb][3][ri] - mn - 8.0f);
+            lsum += p0v + p1v;
+            lsum256 += p2v + p3v;
+            // (scale, zero) pairs of tokens 64cb + 4r + {0..3}
+            const half2v sv01 = as_h2(__builtin_amdgcn_perm(vm[1], vm[0], 0x05040100u));
+            const half2v zv01 = as_h2(__builtin_amdgcn_perm(vm[1], vm[0], 0x07060302u));
+            const half2v sv23 = as_h2(__builtin_amdgcn_perm(vm[3], vm[2], 0x05040100u));
+            const half2v zv23 = as_h2(__builtin_amdgcn_perm(vm[3], vm[2], 0x07060302u));
+            const half2v a01 = as_h2(pack_h2(p0v, p1v)) * sv01;
+            const half2v a23 = as_h2(pack_h2(p2v, p3v)) * sv23;
+            const half2v w01 = zv01 + one1024;
+            const half2v w23 = __builtin_elementwise_fma(zv23, s256, one1024);
+            bsum = __builtin_amdgcn_fdot2(a01, w01, bsum, false);
+            bsum = __builtin_amdgcn_fdot2(a23, w23, bsum, false);
+            *(uint2 *)(pbuf + h * 128 + 64 * cb + 4 * r) = make_uint2(as_u(a01), as_u(a23));
+        }
+        W.l_run[j] = W.l_run[j] * alpha[j] + lsum + 256.0f * lsum256;
+        vbias[j] = row_sum16(bsum);
+    }
+
+    // ---------------- PV: O = O * alpha - bias + P' V
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int j = 0; j < HPL; ++j)
+                W.O[cb][a][j * RSTEP] = W.O[cb][a][j * RSTEP] * alpha[j] - vbias[j];
+    // P' rows are read with inline asm: the compiler cannot tell this stage
+    // apart from the one the next page is streaming into and would otherwise
+    // wait for that prefetch (vmcnt(0)) here.  LDS executes a wave's
+    // operations in order, so the reads see the writes above; lgkmcnt(0)
+    // makes their results available.
+    half8 Ap[4];
+    {
+        const unsigned addr = (unsigned)(uintptr_t)(pbuf + W.prow * 128 + 8 * q);
+        asm volatile("ds_read_b128 %0, %4\n\t"
+                     "ds_read_b128 %1, %4 offset:64\n\t"
+                     "ds_read_b128 %2, %4 offset:128\n\t"
+                     "ds_read_b128 %3, %4 offset:192\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=v"(Ap[0]), "=v"(Ap[1]), "=v"(Ap[2]), "=v"(Ap[3])
+                     : "v"(addr)
+                     : "memory");
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            W.O[cb][0] = mfma(Ap[s], codes_to_half8<0>(vraw[s][cb], cm), W.O[cb][0]);
+            W.O[cb][1] = mfma(Ap[s], codes_to_half8<1>(vraw[s][cb], cm), W.O[cb][1]);
+            W.O[cb][2] = mfma(Ap[s], codes_to_half8<2>(vraw[s][cb], cm), W.O[cb][2]);
+            W.O[cb][3] = mfma(Ap[s], codes_to_half8<3>(vraw[s][cb], cm), W.O[cb][3]);
+        }
+}
+
+// Occupancy target (waves per SIMD): two waves for GQA groups of 4 and 8
+// (256 registers each, measured faster than one wave with no register cap),
+// one for 16 heads, whose accumulators do not fit in 256.
+template <int GQ>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(GQ <= 8 ? 2 : 1)))
+void decode_mfma_kernel(DecodeParams p)
+{
+    constexpr int HPL = GQ / 4;
+    constexpr int RSTEP = 4 / HPL;
     constexpr int ROWS_PER_HEAD = 16 / GQ;
-    __shared__ __attribute__((aligned(16))) unsigned char stage[kStage];
-    __shared__ __attribute__((aligned(16))) _Float16 pbuf[(GQ + 1) * 128];  // + zero row
-    __shared__ int rank_chan[32];
+    // Two LDS stages: the wave computes on one while the next page streams
+    // into the other with global_load_lds.
+    __shared__ __attribute__((aligned(16))) unsigned char stage0[kStage];
+    __shared__ __attribute__((aligned(16))) unsigned char stage1[kStage];
 
     const int lane = threadIdx.x, q = lane >> 4, r = lane & 15;
     const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
@@ -263,7 +494,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p)
 
     if (split == p.n_splits) {
         float m[GQ], l[GQ], O[GQ][2];
-        fp16_segments<GQ>(p, b, kh, (float *)stage, (float *)pbuf, m, l, O);
+        fp16_segments<GQ>(p, b, kh, (float *)stage0, (float *)stage1, m, l, O);
         for (int g = 0; g < GQ; ++g) {
             const int64_t row = ((int64_t)b * p.Hq + kh * GQ + g) * NS + split;
             *(float2 *)(p.ws_o + row * 128 + 2 * lane) = make_float2(O[g][0], O[g][1]);
@@ -281,7 +512,9 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p)
     const int p0 = split * p.pages_per_split;
     const int p1 = poison ? p0 : min(np, p0 + p.pages_per_split);
 
-    // rank -> channel map of this KV head (the inverse of boost_idx).
+    // rank -> channel map of this KV head (inverse of boost_idx), built in
+    // stage1 before any page lands there.
+    int *rank_chan = (int *)stage1;
     if (lane < 32)
         rank_chan[lane] = 0;
     __syncthreads();
@@ -290,234 +523,140 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeParams p)
         if (bi < Dk)
             rank_chan[bi] = d;
     }
-    for (int e = lane; e < 128; e += 64)
-        pbuf[GQ * 128 + e] = (_Float16)0.0f;
     __syncthreads();
 
+    WaveState<GQ> W;
     // Static halves of the QK A operand: q * sm_scale * log2(e) / 2^e for the
     // lane's 8 channels of every K-step; zero on rows that carry no head.
     const bool head_row = (r % ROWS_PER_HEAD) == 0;
     const int hr = r / ROWS_PER_HEAD;  // head of MFMA row r
-    const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + (head_row ? hr : 0)) * p.q_s_head;
-    const float qscale = p.sm_scale * kLog2e;
-    u32x4 qv[4], qvh;
-    int hch[8];
+    W.prow = hr;
+    const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + hr) * p.q_s_head;
+    const float qscale = head_row ? p.sm_scale * kLog2e : 0.0f;
+    {
+        u32x4 qraw[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < 4; ++s)
+            qraw[s] = *(const u32x4 *)(qrow + 32 * s + 8 * q);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            W.hch[i] = rank_chan[8 * q + i];
+        _Float16 qh[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            qh[i] = *(const _Float16 *)(qrow + W.hch[i]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const half2v h = as_h2(qraw[s][j]);
+                const float inv = (j & 1) ? qscale * (1.0f / 256.0f) : qscale;
+                W.qv[s][j] = pack_h2((float)h[0] * inv, (float)h[1] * inv);
+            }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int c = 32 * s + 8 * q + 2 * j;
-            const float inv = (j & 1) ? (1.0f / 256.0f) : 1.0f;
-            qv[s][j] = head_row ? pack_h2(h2f(qrow[c]) * qscale * inv, h2f(qrow[c + 1]) * qscale * inv) : 0u;
+            const float inv = (j & 1) ? qscale * (4.0f / 256.0f) : qscale * 4.0f;
+            const int r0 = 8 * q + 2 * j;
+            W.qvh[j] = pack_h2(r0 < Dk ? (float)qh[2 * j] * inv : 0.0f,
+                               r0 + 1 < Dk ? (float)qh[2 * j + 1] * inv : 0.0f);
         }
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-        hch[i] = rank_chan[8 * q + i];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float inv = (j & 1) ? (4.0f / 256.0f) : 4.0f;
-        const int r0 = 8 * q + 2 * j;
-        const float a0 = (head_row && r0 < Dk) ? h2f(qrow[hch[2 * j]]) * qscale * inv : 0.0f;
-        const float a1 = (head_row && r0 + 1 < Dk) ? h2f(qrow[hch[2 * j + 1]]) * qscale * inv : 0.0f;
-        qvh[j] = pack_h2(a0, a1);
     }
-    // B operand of the QK bias tile for the high rows: -1024 everywhere.
-    const half8 bw_hi = __builtin_bit_cast(half8, u32x4{0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u});
-    const half2v neg1024 = as_h2(0xE400E400u);
-    const half2v negs_lo = as_h2(0xBC00BC00u);   // -1
-    const half2v negs_hi = as_h2(0xDC00DC00u);   // -256
-    const half2v one1024 = as_h2(0x64006400u);
-    const half2v s256 = as_h2(0x5C005C00u);      // 256
-
-    // tr8 source address of this lane inside a 128 x 32 B region.
-    const int rho = ((r >> 1) & 4) | (((r >> 1) & 1) << 1) | (((r >> 1) >> 1) & 1);
-    const int tr_row = 8 * q + rho;
-    const int tr_base0 = 32 * tr_row + 16 * (0 ^ (q & 1)) + 8 * (r & 1);
-    const int tr_base1 = 32 * tr_row + 16 * (1 ^ (q & 1)) + 8 * (r & 1);
-
-    float m_run[HPL], l_run[HPL];
-    f32x4 O[2][4];
+    // tr8 source address of this lane inside a 128 x 32 B region: rows
+    // 8q + rho(r/2) (rho swaps the middle pair so extracted halves come out in
+    // natural order), byte column 8 (r & 1) of chunk cb ^ (q & 1).
+    {
+        const int i = r >> 1;
+        const int rho = (i & 4) | ((i & 1) << 1) | ((i >> 1) & 1);
+        const int tr_row = 8 * q + rho;
+        W.tr_base0 = 32 * tr_row + 16 * (0 ^ (q & 1)) + 8 * (r & 1);
+        W.tr_base1 = 32 * tr_row + 16 * (1 ^ (q & 1)) + 8 * (r & 1);
+    }
 #pragma unroll
     for (int j = 0; j < HPL; ++j) {
-        m_run[j] = -__builtin_inff();
-        l_run[j] = 0.0f;
+        W.m_run[j] = -__builtin_inff();
+        W.l_run[j] = 0.0f;
     }
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
         for (int a = 0; a < 4; ++a)
-            O[cb][a] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            W.O[cb][a] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    __syncthreads();  // rank_chan reads done before stage1 is overwritten
 
-    PageRegs R;
+    // Page ids of this split (at most 64, see choose_pages_per_split), one
+    // per lane, loaded once and read back with v_readlane so no page waits on
+    // a dependent global load.
+    const int ids = p0 + lane < p1 ? p.block_table[b * p.bt_stride + p0 + lane] : 0;
+    auto page_ok = [&](int32_t page) { return page >= 0 && page < p.num_pool_pages; };
+    auto page_at = [&](int pi) -> int32_t { return __builtin_amdgcn_readlane(ids, pi - p0); };
+
     if (p0 < p1) {
-        const int32_t page = p.block_table[b * p.bt_stride + p0];
-        if (page < 0 || page >= p.num_pool_pages)
+        const int32_t page = page_at(p0);
+        if (!page_ok(page))
             poison = true;
-        else {
-            load_page(R, page_src(p, (int64_t)page * p.Hkv + kh), lane, Dk);
-            store_page(stage, R, lane, Dk);
+        else
+            issue_page(stage0, page_src(p, (int64_t)page * p.Hkv + kh), lane, Dk);
+    }
+    // Pages alternate between the stages; each step prefetches the next page
+    // into the other stage, waits for its own page's loads, and computes.
+    for (int pi = p0; pi < p1 && !poison; pi += 2) {
+        {
+            bool next = false;
+            if (pi + 1 < p1) {
+                const int32_t page = page_at(pi + 1);
+                if (!page_ok(page))
+                    poison = true;
+                else {
+                    issue_page(stage1, page_src(p, (int64_t)page * p.Hkv + kh), lane, Dk);
+                    next = true;
+                }
+            }
+            if (next)
+                wait_vmcnt<kLoadsPerPage>();
+            else
+                wait_vmcnt<0>();
+            compute_page<GQ>(W, stage0, lane, Dk);
+            if (!next)
+                break;
+        }
+        {
+            bool next = false;
+            if (pi + 2 < p1) {
+                const int32_t page = page_at(pi + 2);
+                if (!page_ok(page))
+                    poison = true;
+                else {
+                    issue_page(stage0, page_src(p, (int64_t)page * p.Hkv + kh), lane, Dk);
+                    next = true;
+                }
+            }
+            if (next)
+                wait_vmcnt<kLoadsPerPage>();
+            else
+                wait_vmcnt<0>();
+            compute_page<GQ>(W, stage1, lane, Dk);
         }
     }
-    for (int pi = p0; pi < p1 && !poison; ++pi) {
-        bool have_next = false;
-        if (pi + 1 < p1) {
-            const int32_t page = p.block_table[b * p.bt_stride + pi + 1];
-            if (page < 0 || page >= p.num_pool_pages)
-                poison = true;  // finish this page, then stop
-            else {
-                load_page(R, page_src(p, (int64_t)page * p.Hkv + kh), lane, Dk);
-                have_next = true;
-            }
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this page's stores are in LDS
-
-        // ---------------- QK A operands and bias tile
-        half8 A[4], Ahi;
-        f32x4 bias = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const u32x4 ks = *(const u32x4 *)(stage + kMeta + 2 * (32 * s + 8 * q));
-            const u32x4 kz = *(const u32x4 *)(stage + kMeta + 256 + 2 * (32 * s + 8 * q));
-            u32x4 av, bw;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                av[j] = as_u(as_h2(qv[s][j]) * as_h2(ks[j]));
-                bw[j] = as_u(__builtin_elementwise_fma(as_h2(kz[j]), (j & 1) ? negs_hi : negs_lo, neg1024));
-            }
-            A[s] = __builtin_bit_cast(half8, av);
-            bias = mfma(A[s], __builtin_bit_cast(half8, bw), bias);
-        }
-        if (Dk > 0) {
-            u32x4 ksh, av;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                half2v h;
-                h[0] = *(const _Float16 *)(stage + kMeta + 2 * hch[2 * j]);
-                h[1] = *(const _Float16 *)(stage + kMeta + 2 * hch[2 * j + 1]);
-                ksh[j] = as_u(h);
-                av[j] = as_u(as_h2(qvh[j]) * h);
-            }
-            Ahi = __builtin_bit_cast(half8, av);
-            bias = mfma(Ahi, bw_hi, bias);
-        }
-
-        // ---------------- QK token tiles: S[cb][a] covers tokens 64cb + 4r + a
-        f32x4 S[2][4];
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-                S[cb][a] = bias;
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const i32x2 raw = tr8(stage + kKlo + 1024 * s + (cb ? tr_base1 : tr_base0));
-                S[cb][0] = mfma(A[s], codes_to_half8<0>(raw), S[cb][0]);
-                S[cb][1] = mfma(A[s], codes_to_half8<1>(raw), S[cb][1]);
-                S[cb][2] = mfma(A[s], codes_to_half8<2>(raw), S[cb][2]);
-                S[cb][3] = mfma(A[s], codes_to_half8<3>(raw), S[cb][3]);
-            }
-        if (Dk > 0) {
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const i32x2 raw = tr8(stage + kKhi + (cb ? tr_base1 : tr_base0));
-                S[cb][0] = mfma(Ahi, codes_to_half8<0>(raw), S[cb][0]);
-                S[cb][1] = mfma(Ahi, codes_to_half8<1>(raw), S[cb][1]);
-                S[cb][2] = mfma(Ahi, codes_to_half8<2>(raw), S[cb][2]);
-                S[cb][3] = mfma(Ahi, codes_to_half8<3>(raw), S[cb][3]);
-            }
-        }
-
-        // ---------------- online softmax and P' (fp16) with the PV bias
-        const u32x4 vm0 = *(const u32x4 *)(stage + kMeta + 512 + 4 * (4 * r));
-        const u32x4 vm1 = *(const u32x4 *)(stage + kMeta + 512 + 4 * (64 + 4 * r));
-        float alpha[HPL], vbias[HPL];
-#pragma unroll
-        for (int j = 0; j < HPL; ++j) {
-            const int ri = j * RSTEP;
-            float mx = S[0][0][ri];
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-                for (int a = 0; a < 4; ++a)
-                    mx = fmaxf(mx, S[cb][a][ri]);
-            mx = row_max16(mx);
-            const float mn = fmaxf(m_run[j], mx);
-            alpha[j] = __builtin_amdgcn_exp2f(m_run[j] - mn);
-            m_run[j] = mn;
-            float lsum = 0.0f, lsum256 = 0.0f, bsum = 0.0f;
-            const int h = q * HPL + j;
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const u32x4 vm = cb ? vm1 : vm0;
-                const float p0v = __builtin_amdgcn_exp2f(S[cb][0][ri] - mn);
-                const float p1v = __builtin_amdgcn_exp2f(S[cb][1][ri] - mn);
-                const float p2v = __builtin_amdgcn_exp2f(S[cb][2][ri] - mn - 8.0f);  // p / 256
-                const float p3v = __builtin_amdgcn_exp2f(S[cb][3][ri] - mn - 8.0f);
-                lsum += p0v + p1v;
-                lsum256 += p2v + p3v;
-                // (scale, zero) pairs of tokens 64cb + 4r + {0..3}
-                const half2v sv01 = as_h2(__builtin_amdgcn_perm(vm[1], vm[0], 0x05040100u));
-                const half2v zv01 = as_h2(__builtin_amdgcn_perm(vm[1], vm[0], 0x07060302u));
-                const half2v sv23 = as_h2(__builtin_amdgcn_perm(vm[3], vm[2], 0x05040100u));
-                const half2v zv23 = as_h2(__builtin_amdgcn_perm(vm[3], vm[2], 0x07060302u));
-                const half2v a01 = as_h2(pack_h2(p0v, p1v)) * sv01;
-                const half2v a23 = as_h2(pack_h2(p2v, p3v)) * sv23;
-                const half2v w01 = zv01 + one1024;
-                const half2v w23 = __builtin_elementwise_fma(zv23, s256, one1024);
-                bsum = __builtin_amdgcn_fdot2(a01, w01, bsum, false);
-                bsum = __builtin_amdgcn_fdot2(a23, w23, bsum, false);
-                *(uint2 *)(pbuf + h * 128 + 64 * cb + 4 * r) = make_uint2(as_u(a01), as_u(a23));
-            }
-            l_run[j] = l_run[j] * alpha[j] + lsum + 256.0f * lsum256;
-            vbias[j] = row_sum16(bsum);
-        }
-
-        // ---------------- PV: O = O * alpha - bias + P' V
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-#pragma unroll
-                for (int j = 0; j < HPL; ++j)
-                    O[cb][a][j * RSTEP] = O[cb][a][j * RSTEP] * alpha[j] - vbias[j];
-        const int prow = head_row ? hr : GQ;  // the zero row for MFMA rows without a head
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const half8 Ap = *(const half8 *)(pbuf + prow * 128 + 32 * s + 8 * q);
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const i32x2 raw = tr8(stage + kVal + 1024 * s + (cb ? tr_base1 : tr_base0));
-                O[cb][0] = mfma(Ap, codes_to_half8<0>(raw), O[cb][0]);
-                O[cb][1] = mfma(Ap, codes_to_half8<1>(raw), O[cb][1]);
-                O[cb][2] = mfma(Ap, codes_to_half8<2>(raw), O[cb][2]);
-                O[cb][3] = mfma(Ap, codes_to_half8<3>(raw), O[cb][3]);
-            }
-        }
-        if (have_next) {
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // every LDS read of this page has returned
-            store_page(stage, R, lane, Dk);
-        }
-    }
+    if (poison)
+        wait_vmcnt<0>();  // no load may still be writing LDS when the wave retires
 
     // ---------------------------------------------------- write partial
 #pragma unroll
     for (int j = 0; j < HPL; ++j) {
-        const float l = row_sum16(l_run[j]);
+        const float l = row_sum16(W.l_run[j]);
         const int h = q * HPL + j;
         const int64_t row = ((int64_t)b * p.Hq + kh * GQ + h) * NS + split;
         float *o = p.ws_o + row * 128;
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-            float4 v = make_float4(O[cb][0][j * RSTEP], O[cb][1][j * RSTEP], O[cb][2][j * RSTEP],
-                                   O[cb][3][j * RSTEP]);
+            float4 v = make_float4(W.O[cb][0][j * RSTEP], W.O[cb][1][j * RSTEP], W.O[cb][2][j * RSTEP],
+                                   W.O[cb][3][j * RSTEP]);
             if (poison)
                 v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
             *(float4 *)(o + 64 * cb + 4 * r) = v;
         }
         if (r == 0) {
-            p.ws_ml[2 * row] = poison ? __builtin_nanf("") : m_run[j];
+            p.ws_ml[2 * row] = poison ? __builtin_nanf("") : W.m_run[j];
             p.ws_ml[2 * row + 1] = l;
         }
     }

@@ -15,7 +15,8 @@ from typing import Optional
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libkitty_hip.so")
+# KITTY_HIP_LIBRARY selects another build of the same ABI (e.g. a tuning variant).
+LIB_PATH = os.environ.get("KITTY_HIP_LIBRARY") or os.path.join(_HERE, "libkitty_hip.so")
 
 KITTY_ABI_VERSION = 1
 KITTY_OK = 0

@@ -55,9 +55,12 @@ def test_invalid_arguments_are_rejected_without_launch():
 
 def test_workspace_size_formula():
     from kitty.kernels.ops import decode_workspace_bytes
-    # config 3: 16 x 8 pairs, 255 pages -> 16 splits of 16 pages (+1 FP16 split)
+    # config 3 on 256 CUs (2048 resident waves): 128 pairs x 16 waves ->
+    # 15 splits of 17 pages + 1 FP16 split per pair
     n = decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255)
-    assert n == 16 * 32 * 17 * (128 + 2) * 4
+    assert n == 16 * 32 * 16 * (128 + 2) * 4
+    n = decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255, pages_per_split=200)  # capped at 64
+    assert n == 16 * 32 * (4 + 1) * (128 + 2) * 4
 
 
 def test_cpu_tensors_rejected_no_fallback():
