@@ -6,11 +6,19 @@ device tensors; there is no CPU compute path.
 """
 from .config import KittyConfig
 from .layout import Page, PageCentricKVLayoutManager
+from .pipeline import KittyInferencePipeline
+from .attention import KittyPagedAttention, KittyAttentionFactory
 
 __version__ = "0.1.0"
+__description__ = (
+    "2-bit KV Cache Quantization with per-channel boosted precision and Dense-Sparse memory "
+    "decomposition; MI355X HIP kernels.")
 
 __all__ = [
     "KittyConfig",
     "Page",
     "PageCentricKVLayoutManager",
+    "KittyInferencePipeline",
+    "KittyPagedAttention",
+    "KittyAttentionFactory",
 ]

@@ -143,7 +143,7 @@ class DecodePlan:
                  tail_k: torch.Tensor, tail_v: torch.Tensor, tail_len: torch.Tensor,
                  max_pages: Optional[int] = None, pages_per_split: int = 0,
                  sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                 workspace: Optional[torch.Tensor] = None):
+                 workspace: Optional[torch.Tensor] = None, boost_unique: Optional[bool] = None):
         dev = _hip.require_device(q, block_table, num_pages, key_baseline, key_boost, key_meta, value_pool,
                                   value_meta, boost_idx, sink_k, sink_v, sink_len, tail_k, tail_v, tail_len)
         B, Hq, D = q.shape
@@ -188,7 +188,9 @@ class DecodePlan:
         a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, D
         a.page_tokens, a.d_boost = G4 * 4, key_boost.shape[2]
         a.max_pages, a.pages_per_split = int(max_pages), int(pages_per_split)
-        a.flags = _hip.KITTY_DECODE_UNIQUE_BOOST_ROWS if boost_rows_unique(boost_idx, key_boost.shape[2]) else 0
+        if boost_unique is None:
+            boost_unique = boost_rows_unique(boost_idx, key_boost.shape[2])
+        a.flags = _hip.KITTY_DECODE_UNIQUE_BOOST_ROWS if boost_unique else 0
         a.sm_scale = float(1.0 / math.sqrt(D) if sm_scale is None else sm_scale)
         self._L = _hip.load()
         need = ctypes.c_size_t(0)

@@ -113,3 +113,22 @@ def test_pool_override_sizes_multi_layer_pools():
     cfg = _cfg(pool_pages_override=_cfg().max_pages * 2)
     lay = _layout(cfg)
     assert lay.key_baseline.shape[0] == cfg.max_pages * 2
+
+
+def test_pipeline_counters_on_cpu_and_no_cpu_quantisation():
+    """Host bookkeeping works anywhere; a spill needs the HIP kernels and a
+    ROCm device (there is no CPU fallback)."""
+    from kitty import KittyInferencePipeline
+    cfg = _cfg(num_layers=1)
+    lay = _layout(cfg)
+    bi = torch.full((1, cfg.num_kv_heads, cfg.head_dim), cfg.sentinel, dtype=torch.uint8)
+    p = KittyInferencePipeline(cfg, lay, bi)
+    H, D = cfg.num_kv_heads, cfg.head_dim
+    for _ in range(cfg.sink_size + 3):
+        p.push_token(0, torch.randn(H, D).half(), torch.randn(H, D).half())
+    assert p.sink_fill == cfg.sink_size and p.key_qbuf_len == 3 and p.val_local_len == 3
+    ctx = p.get_attention_context(0)
+    assert ctx["sink_k"].shape == (H, cfg.sink_size, D) and ctx["key_qbuf"].shape == (H, 3, D)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        for _ in range(cfg.q_buffer_size):
+            p.push_token(0, torch.randn(H, D).half(), torch.randn(H, D).half())

@@ -1,0 +1,211 @@
+"""Pipeline and drop-in module on the GPU.
+
+* the reference's pipeline-state tests (tests/test_attention.py:57-126);
+* page bytes after spills are the oracle quantisation of the same tokens;
+* KittyPagedAttention decode end to end against the oracle computed from the
+  raw token history (sinks, pages and tail derived independently), including
+  BASELINE config 1 (B1, 8Q/8KV, d128, context 1024, outlier key channels).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from kvgen import calibrate_boost_idx, outlier_keys
+
+pytestmark = pytest.mark.gpu
+
+
+def _cfg(**kw):
+    from kitty import KittyConfig
+    d = dict(num_layers=1, num_kv_heads=2, head_dim=16, q_buffer_size=8, sink_size=4, local_value_window=8,
+             boost_rate=0.25, device="cuda:0")
+    d.update(kw)
+    return KittyConfig(**d)
+
+
+def _boost(cfg):
+    bi = torch.full((cfg.num_layers, cfg.num_kv_heads, cfg.head_dim), cfg.sentinel, dtype=torch.uint8)
+    for i in range(cfg.d_boost):
+        bi[:, :, i] = i
+    return bi
+
+
+def _pipe(cfg, bi=None):
+    from kitty import KittyInferencePipeline, PageCentricKVLayoutManager
+    bi = _boost(cfg) if bi is None else bi
+    lay = PageCentricKVLayoutManager(cfg, bi)
+    return KittyInferencePipeline(cfg, lay, bi), lay, bi
+
+
+def _tok(H, D, gen):
+    return torch.randn(H, D, generator=gen).half(), torch.randn(H, D, generator=gen).half()
+
+
+def test_reference_pipeline_state(dev):
+    cfg = _cfg()
+    H, D, G, S = cfg.num_kv_heads, cfg.head_dim, cfg.q_buffer_size, cfg.sink_size
+    gen = torch.Generator().manual_seed(0)
+    p, lay, _ = _pipe(cfg)
+    for _ in range(S):
+        p.push_token(0, *_tok(H, D, gen))
+    assert p.sink_fill == S and p.key_qbuf_len == 0           # test_attention.py:57-68
+    for _ in range(3):
+        p.push_token(0, *_tok(H, D, gen))
+    assert p.key_qbuf_len == 3 and p.val_local_len == 3       # :70-84
+    for _ in range(G - 3):
+        p.push_token(0, *_tok(H, D, gen))
+    assert p.key_qbuf_len == 0 and len(lay.get_page_list(0, 0)) == 1   # :86-99
+    for _ in range(2 * G):
+        p.push_token(0, *_tok(H, D, gen))
+    assert len(lay.get_page_list(0, 0)) == 3                  # :115-126
+    p.reset_sequence(0)
+    assert p.sink_fill == 0 and p.key_qbuf_len == 0 and lay.memory_stats()["pages_used"] == 0  # :101-113
+
+
+def test_spilled_pages_are_bit_exact(dev):
+    cfg = _cfg(num_layers=2, head_dim=128, q_buffer_size=128, sink_size=32, boost_rate=0.125, max_batch_size=3)
+    L, H, D, G, S = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.q_buffer_size, cfg.sink_size
+    gen = torch.Generator().manual_seed(1)
+    bi = torch.stack([torch.stack([torch.full((D,), cfg.sentinel, dtype=torch.uint8) for _ in range(H)])
+                      for _ in range(L)])
+    for l in range(L):
+        for h in range(H):
+            bi[l, h, torch.randperm(D, generator=gen)[:cfg.d_boost]] = torch.arange(cfg.d_boost, dtype=torch.uint8)
+    p, lay, _ = _pipe(cfg, bi)
+    n_tok = {0: S + 2 * G + 5, 1: S + G, 2: S + 3}
+    hist = {s: [] for s in n_tok}
+    for t in range(max(n_tok.values())):
+        ids = [s for s in n_tok if t < n_tok[s]]
+        for l in range(L):
+            k = torch.randn(len(ids), H, D, generator=gen).half()
+            v = torch.randn(len(ids), H, D, generator=gen).half()
+            p.push_tokens(l, k, v, ids)
+            for i, s in enumerate(ids):
+                hist[s].append((l, k[i], v[i]))
+    torch.cuda.synchronize()
+    kb, kh, km, vp, vm = [t.cpu().numpy() for t in (lay.key_baseline, lay.key_boost, lay.key_metadata,
+                                                     lay.value_pool, lay.value_metadata)]
+    for s in n_tok:
+        for l in range(L):
+            toks = [(k, v) for (ll, k, v) in hist[s] if ll == l]
+            pages = lay.get_page_list(s, l)
+            assert len(pages) == (n_tok[s] - S) // G
+            for pi, ph in enumerate(pages):
+                blk = toks[S + pi * G: S + (pi + 1) * G]
+                K = torch.stack([k for k, _ in blk]).numpy()   # (G, H, D)
+                V = torch.stack([v for _, v in blk]).numpy()
+                for h in range(H):
+                    e = O.quantize_key(K[:, h].T.copy(), bi[l, h].numpy(), cfg.d_boost, cfg.sentinel)
+                    assert np.array_equal(kb[ph, h], e[0]) and np.array_equal(kh[ph, h], e[1])
+                    assert np.array_equal(km[ph, h, 0].astype(np.float32), e[2].astype(np.float32))
+                    assert np.array_equal(km[ph, h, 1].astype(np.float32), e[3].astype(np.float32))
+                    ev = O.quantize_value(V[:, h].copy())
+                    assert np.array_equal(vp[ph, h], ev[0])
+                    assert np.array_equal(vm[ph, h, :, 0].astype(np.float32), ev[1].astype(np.float32))
+
+
+def _oracle_from_history(K, V, q, S, G, bi, d_boost, sentinel, Hq, H, D):
+    """Independent oracle: sinks / pages / tail cut from the raw token history."""
+    T = K.shape[0]
+    ns = min(S, T)
+    npg = max(0, (T - S) // G)
+    P = max(npg, 1)
+    kb = np.zeros((P, H, D, G // 4), np.uint8)
+    kh = np.zeros((P, H, d_boost, G // 4), np.uint8)
+    km = np.zeros((P, H, 2, D), np.float16)
+    vp = np.zeros((P, H, G, D // 4), np.uint8)
+    vm = np.zeros((P, H, G, 2), np.float16)
+    for pi in range(npg):
+        blk = slice(S + pi * G, S + (pi + 1) * G)
+        for h in range(H):
+            kb[pi, h], kh[pi, h], km[pi, h, 0], km[pi, h, 1] = O.quantize_key(K[blk, h].T.copy(), bi[h], d_boost,
+                                                                               sentinel)
+            vp[pi, h], vm[pi, h, :, 0], vm[pi, h, :, 1] = O.quantize_value(V[blk, h].copy())
+    tail = slice(S + npg * G, T)
+    return O.paged_attention(q, np.arange(npg), kb, kh, km, vp, vm, bi, d_boost,
+                             K[:ns].transpose(1, 0, 2).copy(), V[:ns].transpose(1, 0, 2).copy(),
+                             K[tail].transpose(1, 0, 2).copy(), V[tail].transpose(1, 0, 2).copy(), Hq, H, D)
+
+
+def _close(got, ref):
+    got, ref = np.asarray(got, np.float32), np.asarray(ref, np.float32)
+    assert np.isfinite(got).all()
+    excess = np.abs(got - ref) - (2e-3 + 1e-2 * np.abs(ref))
+    assert (excess <= 0).all(), f"max |diff| {np.abs(got - ref).max():.3g}"
+
+
+def test_config1_module_decode_step(dev):
+    """one KittyPagedAttention decode step, B1, 8 Q / 8 KV
+    heads, d128, context 1024 (32 sinks + 7 pages + 96 tail... + the new
+    token), 12.5% INT4 channels from 256 calibration tokens with x8 outliers."""
+    from kitty import KittyAttentionFactory
+    cfg = _cfg(num_kv_heads=8, head_dim=128, q_buffer_size=128, sink_size=32, local_value_window=128,
+               boost_rate=0.125, max_seq_len=2048)
+    H, D, Hq = 8, 128, 8
+    gen = torch.Generator().manual_seed(11)
+    K, chans = outlier_keys(gen, (1024,), H, D, 16, 8.0)
+    V = torch.randn(1024, H, D, generator=gen).half()
+    calib, _ = outlier_keys(gen, (256,), H, D, 16, 8.0, channels=chans)
+    bi = calibrate_boost_idx(calib, cfg.d_boost, cfg.sentinel)
+    layout, pipe, layers = KittyAttentionFactory.from_config(cfg, bi[None], Hq)
+    attn = layers[0]
+    # prefill 1023 tokens, decode the 1024th
+    q0 = torch.randn(1, Hq, 1023, D, generator=gen).half()
+    attn(q0.to(dev), K[:1023].permute(1, 0, 2)[None].to(dev), V[:1023].permute(1, 0, 2)[None].to(dev))
+    q = torch.randn(1, Hq, 1, D, generator=gen).half()
+    out = attn(q.to(dev), K[1023:].permute(1, 0, 2)[None].to(dev), V[1023:].permute(1, 0, 2)[None].to(dev))
+    assert out.shape == (1, Hq, 1, D) and out.dtype == torch.float16
+    ref = _oracle_from_history(K.numpy(), V.numpy(), q[0, :, 0].numpy(), 32, 128, bi.numpy(), cfg.d_boost,
+                               cfg.sentinel, Hq, H, D)
+    _close(out[0, :, 0].cpu().numpy(), ref)
+
+
+def test_batched_module_decode_gqa(dev):
+    """Three sequences of different lengths decoded together through the
+    module (GQA 4, MFMA path), checked per sequence against the oracle."""
+    from kitty import KittyAttentionFactory
+    cfg = _cfg(num_kv_heads=2, head_dim=128, q_buffer_size=128, sink_size=32, boost_rate=0.125,
+               max_seq_len=1024, max_batch_size=3)
+    H, D, Hq = 2, 128, 8
+    gen = torch.Generator().manual_seed(12)
+    bi = torch.full((1, H, D), cfg.sentinel, dtype=torch.uint8)
+    for h in range(H):
+        bi[0, h, torch.randperm(D, generator=gen)[:cfg.d_boost]] = torch.arange(cfg.d_boost, dtype=torch.uint8)
+    layout, pipe, layers = KittyAttentionFactory.from_config(cfg, bi, Hq)
+    attn = layers[0]
+    lens = [300, 161, 40]
+    hist = [[], [], []]
+    steps = max(lens)
+    for t in range(steps):
+        ids = [s for s in range(3) if t < lens[s]]
+        k = torch.randn(len(ids), H, 1, D, generator=gen).half()
+        v = torch.randn(len(ids), H, 1, D, generator=gen).half()
+        q = torch.randn(len(ids), Hq, 1, D, generator=gen).half()
+        out = attn(q.to(dev), k.to(dev), v.to(dev), seq_id=ids)
+        for i, s in enumerate(ids):
+            hist[s].append((k[i, :, 0], v[i, :, 0]))
+        if t in (39, 160, 299):  # last step of some sequence: check everyone in the batch
+            for i, s in enumerate(ids):
+                Kh = torch.stack([a for a, _ in hist[s]]).numpy()
+                Vh = torch.stack([b for _, b in hist[s]]).numpy()
+                ref = _oracle_from_history(Kh, Vh, q[i, :, 0].numpy(), 32, 128, bi[0].numpy(), cfg.d_boost,
+                                           cfg.sentinel, Hq, H, D)
+                _close(out[i, :, 0].cpu().numpy(), ref)
+
+
+def test_prefill_output_is_causal_attention(dev):
+    from kitty import KittyAttentionFactory
+    cfg = _cfg(num_kv_heads=2, head_dim=16, q_buffer_size=8, sink_size=4)
+    gen = torch.Generator().manual_seed(13)
+    layout, pipe, layers = KittyAttentionFactory.from_config(cfg, _boost(cfg), 4)
+    q = torch.randn(1, 4, 21, 16, generator=gen).half()
+    k = torch.randn(1, 2, 21, 16, generator=gen).half()
+    v = torch.randn(1, 2, 21, 16, generator=gen).half()
+    out = layers[0](q.to(dev), k.to(dev), v.to(dev)).float().cpu()
+    ke, ve = k.float().repeat_interleave(2, 1), v.float().repeat_interleave(2, 1)
+    s = (q.float() @ ke.transpose(-1, -2)) / 4.0
+    s = s.masked_fill(torch.triu(torch.ones(21, 21, dtype=torch.bool), 1), float("-inf"))
+    ref = torch.softmax(s, -1) @ ve
+    assert torch.allclose(out, ref, atol=2e-3, rtol=1e-2)
+    assert len(layout.get_page_list(0, 0)) == (21 - 4) // 8 and pipe.key_qbuf_len == (21 - 4) % 8
