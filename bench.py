@@ -178,6 +178,19 @@ def bench_quantize(torch, dev, reps: int = 20) -> dict:
             "GBps": round((read + written) / us / 1e3, 1), "bytes_read": read, "bytes_written": written}
 
 
+def copy_probe(torch, dev) -> int:
+    """A device-to-device copy of known size: its FETCH_SIZE / WRITE_SIZE
+    counters per dispatch calibrate the decode kernel's counter readings."""
+    n = 256 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "dispatches": 5}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -188,6 +201,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-quantize", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 256 MiB device copy 5 times (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one MI355X); "
@@ -199,6 +214,8 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
+    if args.copy_probe:
+        return copy_probe(torch, dev)
     cfg = CONFIGS[args.config]
     log(f"building {args.config} workload ({args.copies} pool copies)")
     w = build_workload(torch, dev, cfg, args.copies)
@@ -249,7 +266,7 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "fp16",
         "data": "synthetic: fp16 N(0,1) K/V with x{:g} outlier key channels, quantised on device".format(
             cfg["outlier"]),
         "config": {"workload": f"{args.config}: B{cfg['B']} Hq{cfg['Hq']} Hkv{cfg['Hkv']} d{D} ctx{cfg['ctx']} "
