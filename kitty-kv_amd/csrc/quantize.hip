@@ -25,6 +25,15 @@ __device__ __forceinline__ float clampf(float v, float lo, float hi)
     return v > hi ? hi : v;
 }
 
+// Zero point clamp with torch's sign of zero: its vectorised maximum(v, 0)
+// returns +0 for v = -0, and every production zero-point vector (D or G a
+// multiple of 16) takes that path.
+__device__ __forceinline__ float zp_clamp(float v, float mq)
+{
+    v = v > 0.0f ? v : 0.0f;
+    return v < mq ? v : mq;
+}
+
 // Codes of one quantisation group share (s, z); returns the 2- or 4-bit code.
 __device__ __forceinline__ uint32_t quant_code(float x, float s, float z, float mq)
 {
@@ -95,7 +104,7 @@ __device__ void quantize_key_block(const QuantLaunch &L, int o, int i, unsigned 
             rng = 1e-8f;
         const float mq = boosted ? 15.0f : 3.0f;                   // :81-82
         const float s = rng / mq;                                  // :84
-        const float z = clampf(__builtin_rintf(-mn / s), 0.0f, mq); // :86-87
+        const float z = zp_clamp(__builtin_rintf(-mn / s), mq);     // :86-87
         uint8_t *low_row = st.key_low + page * st.key_low_s_page + i * st.key_low_s_head + d * st.key_low_s_row;
         for (int j = j0; j < j1; ++j) {                            // :95-110
             uint32_t lo = 0, hi = 0;
@@ -173,7 +182,7 @@ __device__ void quantize_value_block(const QuantLaunch &L, int o, int i, unsigne
     if (rng < 1e-8f)
         rng = 1e-8f;
     const float s = rng / 3.0f;                                    // :67
-    const float z = clampf(__builtin_rintf(-mn / s), 0.0f, 3.0f);  // :69-73
+    const float z = zp_clamp(__builtin_rintf(-mn / s), 3.0f);      // :69-73
     uint8_t *row = st.value + page * st.value_s_page + i * st.value_s_head + t * st.value_s_row;
     for (int j = j0; j < j1; ++j) {                                // :78-88
         uint32_t byte = 0;

@@ -96,6 +96,17 @@ static float clampf(float v, float lo, float hi)
     return v > hi ? hi : v;
 }
 
+/* The zero point's clamp, with the sign of zero torch's vectorised
+ * maximum / minimum give it: max(v, +0) is +0 for v = -0 (the second operand
+ * wins a tie), min(v, mq) keeps v.  Every zero point of a production page
+ * (D, G multiples of 16) goes through that vector path; torch's scalar
+ * remainder loop would keep -0 instead. */
+static float zp_clamp(float v, float mq)
+{
+    v = v > 0.0f ? v : 0.0f;
+    return v < mq ? v : mq;
+}
+
 /* ------------------------------------------------ key quantize (A2) */
 /* key: (D, G) fp16 bits, row-major (channel d, token t) at key[d*G + t].
  * Outputs: t2b (D, G/4), thigh (d_boost, G/4), scale (D,), zero (D,) fp16.
@@ -124,7 +135,7 @@ void kitty_oracle_quantize_key(const uint16_t *key, const uint8_t *boost_idx,
             rng = clamp_min;
         float mq = boosted ? 15.0f : 3.0f;                /* :81-82 */
         float s = rng / mq;                               /* :84 */
-        float zp = clampf(rintf(-mn / s), 0.0f, mq);      /* :86-87 */
+        float zp = zp_clamp(rintf(-mn / s), mq);           /* :86-87 */
         for (int t = 0; t < G; ++t) {                     /* :95-99 */
             float x = kitty_oracle_h2f(row[t]);
             float qf = rintf(x / s) + zp;
@@ -163,7 +174,7 @@ void kitty_oracle_quantize_value(const uint16_t *value, int G, int D,
         if (rng < clamp_min)
             rng = clamp_min;
         float s = rng / 3.0f;                             /* :67 */
-        float zp = clampf(rintf(-mn / s), 0.0f, 3.0f);    /* :69-73 */
+        float zp = zp_clamp(rintf(-mn / s), 3.0f);         /* :69-73 */
         for (int d = 0; d < D; ++d) {                     /* :78-82 */
             float v = kitty_oracle_h2f(row[d]);
             uint8_t c = (uint8_t)clampf(rintf(v / s) + zp, 0.0f, 3.0f);

@@ -183,7 +183,8 @@ def quantize_key_np(key: np.ndarray, boost_idx: np.ndarray, d_boost: int, sentin
     rng = np.maximum(mx - mn, np.float32(1e-8))
     mq = np.where(boosted, np.float32(15.0), np.float32(3.0)).astype(np.float32)
     s = (rng / mq).astype(np.float32)
-    zp = np.minimum(np.maximum(np.rint(-mn / s), np.float32(0)), mq).astype(np.float32)
+    zr = np.rint(-mn / s)
+    zp = np.minimum(np.where(zr > 0, zr, np.float32(0)), mq).astype(np.float32)   # -0 -> +0, as torch
     qf = np.rint(x / s[:, None]) + zp[:, None]
     c = np.minimum(np.maximum(qf, np.float32(0)), mq[:, None]).astype(np.uint8)
     lo = c & 3
@@ -209,7 +210,8 @@ def quantize_value_np(value: np.ndarray):
     mx = v.max(axis=1)
     rng = np.maximum(mx - mn, np.float32(1e-8))
     s = (rng / np.float32(3.0)).astype(np.float32)
-    zp = np.minimum(np.maximum(np.rint(-mn / s), np.float32(0)), np.float32(3)).astype(np.float32)
+    zr = np.rint(-mn / s)
+    zp = np.minimum(np.where(zr > 0, zr, np.float32(0)), np.float32(3)).astype(np.float32)
     c = np.minimum(np.maximum(np.rint(v / s[:, None]) + zp[:, None], np.float32(0)),
                    np.float32(3)).astype(np.uint8)
     packed = np.zeros((G, D // 4), np.uint8)

@@ -183,12 +183,12 @@ def test_c_matches_numpy_restatement():
         a = O.quantize_key(k, bi, dk, dk + 1)
         b = O.quantize_key_np(k, bi, dk, dk + 1)
         assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
-        assert np.array_equal(a[2].astype(np.float32), b[2].astype(np.float32))
-        assert np.array_equal(a[3].astype(np.float32), b[3].astype(np.float32))
+        assert np.array_equal(a[2].view(np.uint16), b[2].view(np.uint16))      # bits, sign of zero included
+        assert np.array_equal(a[3].view(np.uint16), b[3].view(np.uint16))
         assert np.array_equal(O.dequantize_key(*a, bi, dk), O.dequantize_key_np(*a, bi, dk))
         va, vb = O.quantize_value(k.T.copy()), O.quantize_value_np(k.T.copy())
         for x, y in zip(va, vb):
-            assert np.array_equal(np.asarray(x).astype(np.float32), np.asarray(y).astype(np.float32))
+            assert np.array_equal(np.asarray(x).view(np.uint8), np.asarray(y).view(np.uint8))
         assert np.array_equal(O.dequantize_value(*va), O.dequantize_value_np(*va))
 
 
@@ -256,3 +256,33 @@ def test_paged_attention_empty_context_is_zero():
     out = O.paged_attention(c["q"], [], c["kb"], c["kh"], c["km"], c["vp"], c["vm"], c["bi"], 4,
                             c["sk"], c["sv"], c["tk"], c["tv"], 4, 2, 16)
     assert (out.astype(np.float32) == 0).all()
+
+
+def test_zero_point_sign_follows_torch_minimum_maximum():
+    """Where -min/scale rounds to -0.0 (all-positive channels / tokens) the
+    reference stores whatever sign torch.maximum / torch.minimum give
+    (quantize_key.py:86-87, quantize_value.py:69-73).  For zero-point vectors
+    whose length is a multiple of the CPU vector width (every production
+    shape: D, G multiples of 16) torch's vector path returns +0.0; the oracle
+    must store exactly those bits.  torch's own routines decide here."""
+    rng = np.random.default_rng(11)
+    k = (rng.uniform(0.05, 2.0, (32, 16))).astype(np.float16)   # every value > 0
+    k[:, 0] = 0.01                                              # small min -> -min/s in (-0.5, 0)
+    bi = _boost(32, 4, 5)
+    kt = torch.from_numpy(k).float()
+    mq = torch.where(torch.from_numpy(bi) < 5, 15.0, 3.0)
+    sc = (kt.max(1).values - kt.min(1).values).clamp(min=1e-8) / mq
+    zr = (-kt.min(1).values / sc).round()
+    assert torch.signbit(zr).all()                              # every zero point starts as -0.0
+    zt = torch.minimum(torch.maximum(zr, torch.zeros_like(zr)), mq).half()
+    for _, _, s_, z_ in (O.quantize_key(k, bi, 4, 5), O.quantize_key_np(k, bi, 4, 5)):
+        assert np.array_equal(z_.view(np.uint16), zt.numpy().view(np.uint16))
+        assert np.array_equal(s_.view(np.uint16), sc.half().numpy().view(np.uint16))
+    v = k.T.copy()                                              # 16 tokens x 32 channels
+    vt = torch.from_numpy(v).float()
+    svt = (vt.max(1).values - vt.min(1).values).clamp(min=1e-8) / 3.0
+    zr = (-vt.min(1).values / svt).round()
+    assert torch.signbit(zr).any()
+    zvt = torch.minimum(torch.maximum(zr, torch.zeros_like(zr)), torch.full_like(zr, 3.0)).half()
+    for _, _, z_ in (O.quantize_value(v), O.quantize_value_np(v)):
+        assert np.array_equal(np.asarray(z_).view(np.uint16), zvt.numpy().view(np.uint16))

@@ -14,7 +14,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _eq16(a, b):
-    return np.array_equal(np.asarray(a, np.float16).astype(np.float32), np.asarray(b, np.float16).astype(np.float32))
+    """fp16 bit patterns equal (the sign of a zero zero-point included)."""
+    return np.array_equal(np.ascontiguousarray(a, np.float16).view(np.uint16),
+                          np.ascontiguousarray(b, np.float16).view(np.uint16))
 
 
 def _pools(P, H, D, G, Dk, dev):
@@ -80,9 +82,11 @@ def test_small_shapes_and_edge_rows(dev, D, G, Dk, H):
     K[0, 0, :, 1] = 2.5           # constant channel -> fp16 scale underflow
     K[1, 0] = 0.0                 # all-zero block
     K[2, -1, 0, :] = 0.5 * torch.arange(D)  # ties
+    K[2, 0, :, 2] = 0.01 + torch.rand(G, generator=gen)   # positive channel: -min/s rounds to -0.0
     K = K.half()
     V = torch.randn(n, H, G, D, generator=gen).half()
     V[0, 0, 3] = -1.0             # constant token
+    V[1, 0, 5] = (0.01 + torch.rand(D, generator=gen)).half()  # positive token: zero point -0.0 -> +0.0
     bi = torch.full((n, H, D), sentinel, dtype=torch.uint8)
     for o in range(n):
         for h in range(H):
