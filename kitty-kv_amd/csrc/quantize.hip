@@ -1,49 +1,17 @@
-// Batch quantize + dense-sparse pack for gfx950 (subsystem 1 of the hot path).
+// Batch quantize + dense-sparse pack for gfx950 (subsystem 1 of the hot path),
+// shape-generic kernel, plus the page dequantisers and the C entry points.
 //
 // One launch quantises every (key, value) block of a spill.  Workgroup
 // (blockIdx.x = block n, blockIdx.y = 0) packs the key block of n per channel,
-// (n, 1) packs the value block per token.  Arithmetic follows
-// quantize_key_page_torch (kitty/kernels/quantize_key.py:69-124) and
-// quantize_value_page_torch (kitty/kernels/quantize_value.py:58-90) op for op
-// in fp32, so codes, scales and zero points are bit-identical:
-//   rng = max(max - min, 1e-8f);  s = rng / mq;  z = clamp(rint(-min / s), 0, mq)
-//   code = clamp(rint(x / s) + z, 0, mq)            (rint = round half to even)
-// with mq = 15 for boosted key channels (boost_idx[d] < sentinel), else 3.
-// Division is the correctly rounded fp32 '/', and no FMA contraction is
-// allowed in this file.
-#include "common.h"
+// (n, 1) packs the value block per token.  The 128 x 128 production shape goes
+// to quantize_page128.hip instead.  Arithmetic: see quantize.h.
+#include "quantize.h"
 
 #pragma clang fp contract(off)
 
 namespace kitty {
 
 constexpr int kQuantThreads = 256;
-
-__device__ __forceinline__ float clampf(float v, float lo, float hi)
-{
-    v = v < lo ? lo : v;
-    return v > hi ? hi : v;
-}
-
-// Zero point clamp with torch's sign of zero: its vectorised maximum(v, 0)
-// returns +0 for v = -0, and every production zero-point vector (D or G a
-// multiple of 16) takes that path.
-__device__ __forceinline__ float zp_clamp(float v, float mq)
-{
-    v = v > 0.0f ? v : 0.0f;
-    return v < mq ? v : mq;
-}
-
-// Codes of one quantisation group share (s, z); returns the 2- or 4-bit code.
-__device__ __forceinline__ uint32_t quant_code(float x, float s, float z, float mq)
-{
-    return (uint32_t)clampf(__builtin_rintf(x / s) + z, 0.0f, mq);
-}
-
-struct QuantLaunch {
-    kitty_page_store st;
-    kitty_quant_batch qb;
-};
 
 // ---------------------------------------------------------------- keys
 // LDS: tile[t][d] fp16 (G x D), boost row (D), high-bit bytes per channel
@@ -229,7 +197,7 @@ __global__ __launch_bounds__(256) void dequantize_key_kernel(kitty_page_store st
                                                              const uint8_t *boost, void *out, int64_t out_s,
                                                              int fp32)
 {
-    const int D = st.head_dim, G = st.page_tokens, G4 = G / 4;
+    const int D = st.head_dim, G = st.page_tokens;
     for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < D * G; e += gridDim.x * blockDim.x) {
         const int d = e / G, t = e - d * G;
         const int j = t >> 2, k = t & 3;
@@ -307,6 +275,8 @@ extern "C" int kitty_quantize_kv_blocks(const kitty_page_store *store, const kit
     if (nblocks > 0x7fffffff)
         return fail(KITTY_E_INVALID, "too many blocks");
     QuantLaunch L{*store, qb};
+    if (page128_supported(*store, qb))
+        return launch_page128(L, (hipStream_t)stream);
     dim3 grid((unsigned)nblocks, 2);
     hipLaunchKernelGGL(quantize_kv_kernel, grid, dim3(kQuantThreads), lds, (hipStream_t)stream, L);
     return check_launch("quantize_kv_kernel");

@@ -1,0 +1,335 @@
+// Batch quantise + pack for the production page shape D = G = 128 on gfx950.
+//
+// One 256-thread workgroup per (block, role): role 0 packs the key block per
+// channel, role 1 the value block per token.  Thread (tt, cg), tt = 4 * wave
+// + lane / 16 and cg = lane % 16, loads tokens 8tt..8tt+7 x channels
+// 8cg..8cg+7 of the fp16 block with eight 16-byte loads, all issued before any
+// arithmetic (32 KB in flight per workgroup, one 256-byte token row per 16
+// lanes).
+//
+// Keys: packed-fp16 min / max over the thread's 8 tokens, then across lanes
+// 16 and 32 apart, then across the 4 waves in LDS; one thread per channel
+// turns (min, max) into (s, 1/s, z) and the stored fp16 scale / zero point.
+// Values: packed-fp16 (min, -max) over the thread's 8 channels, then across
+// the 16 lanes of a DPP row; lane k of the row computes the parameters of
+// the row's token k.  Parameters go through LDS to the threads that code the
+// elements.  Each thread packs its 8 x 8 codes into 16-bit pieces of the
+// packed rows, the page is assembled in LDS, and the workgroup writes the
+// 4 KB code region with one 16-byte store per thread.
+//
+// Arithmetic is that of quantize.h (bit-exact with the reference); the codes
+// use the multiply-by-reciprocal of rint_quot below, which returns the same
+// integer as rint of the correctly rounded quotient.
+#include "quantize.h"
+
+#pragma clang fp contract(off)
+
+namespace kitty {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+
+// LDS layout (bytes).  The code tile holds 128 rows x 32 B with 16 B of
+// padding after every 8 rows, so the rows a wave writes together (8 apart)
+// fall in different banks.
+__device__ __forceinline__ int tile_off(int row) { return row * 32 + (row >> 3) * 16; }
+constexpr int kTileBytes = 128 * 32 + 16 * 16;          // 4,352
+constexpr int kHighOff = kTileBytes;                    // key high rows, <= 128 x 32 B
+constexpr int kRedOff = kHighOff + 128 * 32;            // key partial min / max: 2 x 4 waves x 128 fp16
+constexpr int kParOff = kRedOff + 2 * 4 * 128 * 2;      // parameters: s, 1/s, z, mq, high row: 5 x 128 x 4 B
+constexpr int kLdsBytes = kParOff + 5 * 128 * 4;        // 13,056
+
+__device__ __forceinline__ h2 as_h2(unsigned w) { return __builtin_bit_cast(h2, w); }
+__device__ __forceinline__ unsigned as_u(h2 v) { return __builtin_bit_cast(unsigned, v); }
+__device__ __forceinline__ h2 hmin(h2 a, h2 b) { return __builtin_elementwise_min(a, b); }
+__device__ __forceinline__ h2 hmax(h2 a, h2 b) { return __builtin_elementwise_max(a, b); }
+
+__device__ __forceinline__ float chan(const u32x4 &v, int c)
+{
+    const unsigned w = v[c >> 1];
+    return h2f((uint16_t)((c & 1) ? (w >> 16) : (w & 0xffffu)));
+}
+
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp(unsigned v)
+{
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+// rint(x / s) of the correctly rounded quotient, without a division per
+// element.  rs = v_rcp(s) is within 1 ulp of 1/s, so y = x * rs is within
+// 2^-22 |x / s| of x / s, and fl(x / s) within 2^-24 |x / s|: while
+// |x / s| < 32 the two are less than 2^-17 apart and round to the same
+// integer unless y lies within 2^-14 of a half-integer, where the quotient is
+// recomputed exactly (about 1 element in 8,000 for smooth data; every tie of
+// grid-aligned data).  For |x / s| >= 32 both round outside [-mq, mq] with
+// the same sign, and the code / zero-point clamps give the same end value.
+// Inputs are finite fp16.
+__device__ __forceinline__ float rint_quot(float x, float s, float rs)
+{
+    const float y = x * rs;
+    float n = __builtin_rintf(y);
+    if (__builtin_expect(__builtin_fabsf(y - n) > 0.5f - 0x1p-14f, 0))
+        n = __builtin_rintf(x / s);
+    return n;
+}
+
+// clamp(n + z, 0, mq) -> code; n and z are small integers, so v_med3 is exact.
+__device__ __forceinline__ unsigned code_of(float n, float z, float mq)
+{
+    return (unsigned)__builtin_amdgcn_fmed3f(n + z, 0.0f, mq);
+}
+
+// Rows t0..t0+7 of a token-major fp16 block, 8 channels each; rows at or past
+// `rows_valid` read as zeros (the reference's zero-padded value rows).
+__device__ __forceinline__ void load_rows(const uint16_t *src, int64_t s_tok, int t0, int rows_valid, u32x4 (&r)[8])
+{
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        r[k] = (t0 + k < rows_valid) ? *(const u32x4 *)(src + (int64_t)(t0 + k) * s_tok) : u32x4{0u, 0u, 0u, 0u};
+}
+
+// Code region of the page (128 rows x 32 B, contiguous): one 16-byte store per thread.
+__device__ __forceinline__ void store_tile(uint8_t *dst, const unsigned char *tile, int tid)
+{
+    *(u32x4 *)(dst + 16 * tid) = *(const u32x4 *)(tile + tile_off(tid >> 1) + 16 * (tid & 1));
+}
+
+// Eight consecutive 32-bit LDS words.  (Each element is copied to a scalar
+// before the bit cast: clang's __builtin_bit_cast of an ext_vector element
+// expression reads element 0.)
+template <typename T>
+__device__ __forceinline__ void read8(const unsigned char *lds, int off, T (&v)[8])
+{
+    const u32x4 a = *(const u32x4 *)(lds + off), b = *(const u32x4 *)(lds + off + 16);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const unsigned wa = a[c], wb = b[c];
+        v[c] = __builtin_bit_cast(T, wa);
+        v[c + 4] = __builtin_bit_cast(T, wb);
+    }
+}
+
+// ------------------------------------------------------------------- keys
+// quantize_key.py:69-124: per channel over the 128 tokens.
+__device__ void key_block(const QuantLaunch &L, int o, int i, int64_t page, unsigned char *lds)
+{
+    const kitty_page_store &st = L.st;
+    const kitty_quant_batch &qb = L.qb;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cg = lane & 15, tt = wave * 4 + (lane >> 4);
+    const int Dk = st.d_boost;
+
+    u32x4 r[8];
+    load_rows(qb.key + o * qb.key_s_outer + i * qb.key_s_inner + 8 * cg, qb.key_s_tok, 8 * tt, 128, r);
+    const int b = tid < 128 ? qb.boost_idx[o * qb.boost_s_outer + i * qb.boost_s_inner + tid] : 0;
+
+    unsigned *high = (unsigned *)(lds + kHighOff);
+    for (int e = tid; e < Dk * 8; e += kThreads)
+        high[e] = 0u; // rows with no channel stay 0 (the reference's zeroed tensor)
+
+    // min / max over the thread's tokens, channel pairs packed in fp16 (:76-77)
+    h2 mn[4], mx[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        mn[j] = mx[j] = as_h2(r[0][j]);
+#pragma unroll
+    for (int k = 1; k < 8; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            mn[j] = hmin(mn[j], as_h2(r[k][j]));
+            mx[j] = hmax(mx[j], as_h2(r[k][j]));
+        }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        mn[j] = hmin(mn[j], as_h2((unsigned)__shfl_xor((int)as_u(mn[j]), 16)));
+        mx[j] = hmax(mx[j], as_h2((unsigned)__shfl_xor((int)as_u(mx[j]), 16)));
+        mn[j] = hmin(mn[j], as_h2((unsigned)__shfl_xor((int)as_u(mn[j]), 32)));
+        mx[j] = hmax(mx[j], as_h2((unsigned)__shfl_xor((int)as_u(mx[j]), 32)));
+    }
+    if (lane < 16) {  // the wave's partial for channels 8cg..8cg+7
+        *(u32x4 *)(lds + kRedOff + wave * 256 + cg * 16) = u32x4{as_u(mn[0]), as_u(mn[1]), as_u(mn[2]), as_u(mn[3])};
+        *(u32x4 *)(lds + kRedOff + 1024 + wave * 256 + cg * 16) =
+            u32x4{as_u(mx[0]), as_u(mx[1]), as_u(mx[2]), as_u(mx[3])};
+    }
+    __syncthreads();
+
+    float *ps = (float *)(lds + kParOff), *prs = ps + 128, *pz = ps + 256, *pmq = ps + 384;
+    int *phr = (int *)(ps + 512);
+    if (tid < 128) {  // channel d = tid
+        const uint16_t *rmn = (const uint16_t *)(lds + kRedOff), *rmx = rmn + 512;
+        float cmn = h2f(rmn[tid]), cmx = h2f(rmx[tid]);
+#pragma unroll
+        for (int w2 = 1; w2 < 4; ++w2) {
+            cmn = __builtin_fminf(cmn, h2f(rmn[w2 * 128 + tid]));
+            cmx = __builtin_fmaxf(cmx, h2f(rmx[w2 * 128 + tid]));
+        }
+        const float mq = b < qb.sentinel ? 15.0f : 3.0f;               // :73, 81-82
+        const float s = range_of(cmn, cmx) / mq;                       // :78-84
+        const float rs = __builtin_amdgcn_rcpf(s);
+        const float z = zp_clamp(rint_quot(-cmn, s, rs), mq);          // :86-87
+        ps[tid] = s;
+        prs[tid] = rs;
+        pz[tid] = z;
+        pmq[tid] = mq;
+        phr[tid] = b < Dk ? b : -1;                                    // :113-116
+        const int64_t m = page * st.key_meta_s_page + i * st.key_meta_s_head + tid;
+        st.key_scale[m] = f2h(s);                                      // :121-122
+        st.key_zero[m] = f2h(z);
+    }
+    __syncthreads();
+
+    float s[8], rs[8], z[8], mq[8];
+    int hr[8];
+    read8(lds, kParOff + 32 * cg, s);
+    read8(lds, kParOff + 512 + 32 * cg, rs);
+    read8(lds, kParOff + 1024 + 32 * cg, z);
+    read8(lds, kParOff + 1536 + 32 * cg, mq);
+    read8(lds, kParOff + 2048 + 32 * cg, hr);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        unsigned lo = 0, hi = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {                                  // :95-103
+            const unsigned q = code_of(rint_quot(chan(r[k], c), s[c], rs[c]), z[c], mq[c]);
+            lo |= (q & 3u) << (2 * k);
+            hi |= ((q >> 2) & 3u) << (2 * k);
+        }
+        // token 8tt+k -> byte 2tt + k/4, bits 2(k%4): a 16-bit piece of row d (:108-110)
+        *(uint16_t *)(lds + tile_off(8 * cg + c) + 2 * tt) = (uint16_t)lo;
+        if (hr[c] >= 0)                                                // :113-119, OR of the rank's channels
+            atomicOr(high + hr[c] * 8 + (tt >> 1), hi << (16 * (tt & 1)));
+    }
+    __syncthreads();
+    store_tile(st.key_low + page * st.key_low_s_page + i * st.key_low_s_head, lds, tid);
+    if (tid < 2 * Dk)
+        *(u32x4 *)(st.key_high + page * st.key_high_s_page + i * st.key_high_s_head + 16 * tid) =
+            *(const u32x4 *)(lds + kHighOff + 16 * tid);
+}
+
+// ----------------------------------------------------------------- values
+// quantize_value.py:58-90: per token over the 128 channels.
+__device__ void value_block(const QuantLaunch &L, int o, int i, int64_t page, unsigned char *lds)
+{
+    const kitty_page_store &st = L.st;
+    const kitty_quant_batch &qb = L.qb;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cg = lane & 15, tt = wave * 4 + (lane >> 4);
+
+    u32x4 r[8];
+    load_rows(qb.value + o * qb.value_s_outer + i * qb.value_s_inner + 8 * cg, qb.value_s_tok, 8 * tt,
+              qb.value_rows, r);
+
+    // (min, -max) of each token over the thread's 8 channels, packed in fp16,
+    // then over the 16 lanes of the DPP row (:63-64)
+    unsigned mm[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const h2 a = hmin(hmin(as_h2(r[k][0]), as_h2(r[k][1])), hmin(as_h2(r[k][2]), as_h2(r[k][3])));
+        const h2 b = hmax(hmax(as_h2(r[k][0]), as_h2(r[k][1])), hmax(as_h2(r[k][2]), as_h2(r[k][3])));
+        // (a.x, -b.x) and (a.y, -b.y): byte-select, then flip the sign of the high half
+        const unsigned lo = __builtin_amdgcn_perm(as_u(b), as_u(a), 0x05040100u) ^ 0x80000000u;
+        const unsigned hi = __builtin_amdgcn_perm(as_u(b), as_u(a), 0x07060302u) ^ 0x80000000u;
+        unsigned v = as_u(hmin(as_h2(lo), as_h2(hi)));
+        v = as_u(hmin(as_h2(v), as_h2(dpp<0x128>(v))));
+        v = as_u(hmin(as_h2(v), as_h2(dpp<0x124>(v))));
+        v = as_u(hmin(as_h2(v), as_h2(dpp<0x122>(v))));
+        mm[k] = as_u(hmin(as_h2(v), as_h2(dpp<0x121>(v))));
+    }
+
+    // lane k < 8 of each row: parameters of token 8tt + k
+    float *ps = (float *)(lds + kParOff), *prs = ps + 128, *pz = ps + 256;
+    if (cg < 8) {
+        unsigned v = mm[0];
+#pragma unroll
+        for (int k = 1; k < 8; ++k)
+            v = cg == k ? mm[k] : v;
+        const float mn = h2f((uint16_t)(v & 0xffffu)), mx = -h2f((uint16_t)(v >> 16));
+        const float s = range_of(mn, mx) / 3.0f;                       // :65-67
+        const float rs = __builtin_amdgcn_rcpf(s);
+        const float z = zp_clamp(rint_quot(-mn, s, rs), 3.0f);         // :69-73
+        const int t = 8 * tt + cg;
+        ps[t] = s;
+        prs[t] = rs;
+        pz[t] = z;
+        const int64_t m = page * st.value_meta_s_page + i * st.value_meta_s_head + 2 * t;
+        *(unsigned *)(st.value_scale + m) = (unsigned)f2h(s) | ((unsigned)f2h(z) << 16);  // :90, interleaved
+    }
+    __syncthreads();
+
+    float s[8], rs[8], z[8];
+    read8(lds, kParOff + 32 * tt, s);
+    read8(lds, kParOff + 512 + 32 * tt, rs);
+    read8(lds, kParOff + 1024 + 32 * tt, z);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        unsigned bits = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c)                                    // :74-88, channel 4j+i at byte j bits 2i
+            bits |= code_of(rint_quot(chan(r[k], c), s[k], rs[k]), z[k], 3.0f) << (2 * c);
+        *(uint16_t *)(lds + tile_off(8 * tt + k) + 2 * cg) = (uint16_t)bits;
+    }
+    __syncthreads();
+    store_tile(st.value + page * st.value_s_page + i * st.value_s_head, lds, tid);
+}
+
+__global__ __launch_bounds__(kThreads) void quantize_page128_kernel(QuantLaunch L)
+{
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+    const int n = blockIdx.x;
+    const int o = n / L.qb.n_inner, i = n - o * L.qb.n_inner;
+    const int64_t page = L.qb.page_ids[o];
+    if (page < 0 || page >= L.st.num_pages || i >= L.st.num_kv_heads)
+        return; // never write outside the pools
+    if (blockIdx.y == 0) {
+        if (L.qb.key)
+            key_block(L, o, i, page, lds);
+    } else if (L.qb.value) {
+        value_block(L, o, i, page, lds);
+    }
+}
+
+static bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+static bool mul(int64_t s, int64_t m) { return s % m == 0; }
+
+bool page128_supported(const kitty_page_store &st, const kitty_quant_batch &qb)
+{
+    if (st.head_dim != 128 || st.page_tokens != 128)
+        return false;
+    if (qb.key) {
+        if (qb.key_s_chan != 1 || !al16(qb.key) || !mul(qb.key_s_outer, 8) || !mul(qb.key_s_inner, 8) ||
+            !mul(qb.key_s_tok, 8))
+            return false;
+        if (st.key_low_s_row != 32 || !al16(st.key_low) || !mul(st.key_low_s_page, 16) ||
+            !mul(st.key_low_s_head, 16))
+            return false;
+        if (st.d_boost > 0 && (st.key_high_s_row != 32 || !al16(st.key_high) || !mul(st.key_high_s_page, 16) ||
+                               !mul(st.key_high_s_head, 16)))
+            return false;
+        if (st.key_meta_s_chan != 1)
+            return false;
+    }
+    if (qb.value) {
+        if (qb.value_s_chan != 1 || !al16(qb.value) || !mul(qb.value_s_outer, 8) || !mul(qb.value_s_inner, 8) ||
+            !mul(qb.value_s_tok, 8))
+            return false;
+        if (st.value_s_row != 32 || !al16(st.value) || !mul(st.value_s_page, 16) || !mul(st.value_s_head, 16))
+            return false;
+        // interleaved (scale, zero) per token, as value_metadata (P, H, G, 2), 4-byte aligned
+        if (st.value_zero != st.value_scale + 1 || st.value_meta_s_tok != 2 || ((uintptr_t)st.value_scale & 3u) ||
+            !mul(st.value_meta_s_page, 2) || !mul(st.value_meta_s_head, 2))
+            return false;
+    }
+    return true;
+}
+
+int launch_page128(const QuantLaunch &L, hipStream_t stream)
+{
+    const int64_t nblocks = (int64_t)L.qb.n_outer * L.qb.n_inner;
+    hipLaunchKernelGGL(quantize_page128_kernel, dim3((unsigned)nblocks, 2), dim3(kThreads), 0, stream, L);
+    return check_launch("quantize_page128_kernel");
+}
+
+} // namespace kitty

@@ -67,15 +67,9 @@ def pool_store(key_baseline: torch.Tensor, key_boost: torch.Tensor, key_meta: to
     return s
 
 
-def quantize_into_pools(store: _hip.PageStore, key: Optional[torch.Tensor], value: Optional[torch.Tensor],
-                        boost_idx: Optional[torch.Tensor], page_ids: torch.Tensor, sentinel: int,
-                        value_rows: Optional[int] = None) -> None:
-    """One launch over an (outer, inner=head) grid of fp16 blocks.
-
-    key / value: (n_outer, n_inner, G, D) fp16 views (any strides);
-    boost_idx: (n_outer, n_inner, D) or (n_inner, D) uint8; page_ids: (n_outer,)
-    int32 device tensor of destination pages.
-    """
+def _quant_batch(store: _hip.PageStore, key: Optional[torch.Tensor], value: Optional[torch.Tensor],
+                 boost_idx: Optional[torch.Tensor], page_ids: torch.Tensor, sentinel: int,
+                 value_rows: Optional[int]) -> Tuple[_hip.QuantBatch, torch.device]:
     ref = key if key is not None else value
     _need(ref is not None, "nothing to quantise")
     dev = _hip.require_device(key, value, boost_idx, page_ids)
@@ -106,8 +100,39 @@ def quantize_into_pools(store: _hip.PageStore, key: Optional[torch.Tensor], valu
     b.n_outer, b.n_inner = n_outer, n_inner
     b.value_rows = G if value_rows is None else int(value_rows)
     b.sentinel = int(sentinel)
-    L = _hip.load()
-    _hip.check(L.kitty_quantize_kv_blocks(ctypes.byref(store), ctypes.byref(b), _hip.stream_ptr(dev)))
+    return b, dev
+
+
+def quantize_into_pools(store: _hip.PageStore, key: Optional[torch.Tensor], value: Optional[torch.Tensor],
+                        boost_idx: Optional[torch.Tensor], page_ids: torch.Tensor, sentinel: int,
+                        value_rows: Optional[int] = None) -> None:
+    """One launch over an (outer, inner=head) grid of fp16 blocks.
+
+    key / value: (n_outer, n_inner, G, D) fp16 views (any strides);
+    boost_idx: (n_outer, n_inner, D) or (n_inner, D) uint8; page_ids: (n_outer,)
+    int32 device tensor of destination pages.
+    """
+    b, dev = _quant_batch(store, key, value, boost_idx, page_ids, sentinel, value_rows)
+    _hip.check(_hip.load().kitty_quantize_kv_blocks(ctypes.byref(store), ctypes.byref(b), _hip.stream_ptr(dev)))
+
+
+class QuantizePlan:
+    """Pre-validated arguments of one batch-quantise launch over fixed tensors
+    (same arguments as :func:`quantize_into_pools`); ``run()`` only enqueues
+    the kernel on the current stream.  The tensors must stay alive and in
+    place while the plan is used."""
+
+    def __init__(self, store: _hip.PageStore, key: Optional[torch.Tensor], value: Optional[torch.Tensor],
+                 boost_idx: Optional[torch.Tensor], page_ids: torch.Tensor, sentinel: int,
+                 value_rows: Optional[int] = None) -> None:
+        self._b, self._dev = _quant_batch(store, key, value, boost_idx, page_ids, sentinel, value_rows)
+        self._store = store
+        self._keep = (key, value, boost_idx, page_ids)
+        self._lib = _hip.load()
+
+    def run(self) -> None:
+        _hip.check(self._lib.kitty_quantize_kv_blocks(ctypes.byref(self._store), ctypes.byref(self._b),
+                                                      _hip.stream_ptr(self._dev)))
 
 
 # --------------------------------------------------------------- decode
