@@ -102,6 +102,47 @@ def test_small_shapes_and_edge_rows(dev, D, G, Dk, H):
                         Dk, sentinel)
 
 
+def _boundary_block(gen, G, D, mq_of_col):
+    """fp16 values at and one fp16 ulp either side of the rounding boundaries
+    (j + 1/2) * s of rint(x / s), for exact (s = 1) and inexact (s = 1/3,
+    2/15, ...) scales; column c is a group with max code mq_of_col[c] whose
+    min / max are pinned to -rng/2, +rng/2."""
+    x = np.zeros((G, D), np.float16)
+    for c in range(D):
+        mq = mq_of_col[c]
+        rng = [float(mq), 1.0, 2.0, 0.7][c % 4]
+        s = np.float32(rng) / np.float32(mq)
+        j = torch.randint(-(mq + 1) // 2, (mq - 1) // 2 + 1, (G,), generator=gen).numpy()
+        t = ((j + 0.5) * s).astype(np.float16)
+        step = torch.randint(-1, 2, (G,), generator=gen).numpy()
+        col = np.where(step == 0, t, np.where(step > 0, np.nextafter(t, np.float16(np.inf)),
+                                              np.nextafter(t, np.float16(-np.inf))))
+        col[0], col[1] = -rng / 2, rng / 2
+        x[:, c] = col
+    return x
+
+
+def test_rounding_boundaries_bit_exact(dev):
+    """Values on and next to the half-integer code boundaries: the kernel's
+    multiply-by-reciprocal codes must take the exact-division path there and
+    match the correctly rounded quotient (quantize_key.py:95, quantize_value.py:79)."""
+    from kitty.kernels.ops import quantize_into_pools
+    D, G, H, Dk = 128, 128, 2, 32
+    gen = torch.Generator().manual_seed(77)
+    bi = torch.full((H, D), Dk + 1, dtype=torch.uint8)
+    for h in range(H):
+        bi[h, torch.randperm(D, generator=gen)[:Dk]] = torch.arange(Dk, dtype=torch.uint8)
+    K = np.stack([_boundary_block(gen, G, D, [15 if bi[h, c] < Dk + 1 else 3 for c in range(D)])
+                  for h in range(H)])                                     # (H, G, D) token-major
+    V = np.stack([_boundary_block(gen, D, G, [3] * G).T.copy() for h in range(H)])  # per-token groups
+    pools, store = _pools(2, H, D, G, Dk, dev)
+    quantize_into_pools(store, torch.from_numpy(K)[None].to(dev), torch.from_numpy(V)[None].to(dev), bi.to(dev),
+                        torch.tensor([1], dtype=torch.int32, device=dev), Dk + 1)
+    torch.cuda.synchronize()
+    for h in range(H):
+        _check_page(pools, 1, h, K[h].T.copy(), V[h], bi[h].numpy(), Dk, Dk + 1)
+
+
 def test_value_rows_zero_padding(dev):
     """Rows past value_rows quantise as zeros (pipeline.py:240-243)."""
     from kitty.kernels.ops import quantize_into_pools
