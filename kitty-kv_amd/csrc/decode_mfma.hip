@@ -7,23 +7,28 @@
 //
 //  QK   S[h][t] = sum_k A[h][k] * B[k][t] with v_mfma_f32_16x16x32_f16.
 //       B: 2-bit codes turned into fp16 by OR-ing them into the mantissa of
-//       1024 (0x6400 | c<<e gives 1024 + c*2^e exactly, 2 VALU ops per 4
-//       codes) after ds_read_b64_tr_b8 transposes the channel-major page in
-//       LDS so each lane holds 8 channels of one byte column (4 tokens).
-//       A: q * scale_k[d] * log2(e)/sqrt(D) / 2^e (fp16), heads on MFMA rows.
-//       The 1024 offsets and the zero points fold into one bias tile:
-//       C_init = -sum_k A[k] * (1024 + 2^e z_k), computed by 5 more MFMAs.
-//       High 2 bits of boosted channels are 16-32 extra reduction rows with
-//       A = 4 * q'[channel(rank)].
+//       1024: the code of token slot a (bits 2a, 2a+1 of a byte) masked in
+//       place gives 1024 + 4^a c exactly, one v_and_or_b32 per two codes, the
+//       odd bytes of each word after one shift by 8.  ds_read_b64_tr_b8
+//       transposes the channel-major page in LDS so each lane holds 8
+//       channels of one byte column (4 tokens, one per slot a).
+//       A: q * scale_k[d] * log2(e)/sqrt(D) (fp16), heads on MFMA rows.
+//       Every MFMA of slot a accumulates 4^a S plus 1024 sum_k A[k]; the
+//       tile starts from -(1024 X + 4^a Y), X = sum_k A[k] and
+//       Y = sum_k A[k] z_k (two bias tiles, 9 MFMAs), and the softmax scales
+//       it by 4^-a.  High 2 bits of boosted channels are 16-32 extra
+//       reduction rows with A = 4 * q'[channel(rank)].
 //  softmax  online, base 2, one DPP row reduction per page.
-//  PV   O[h][d] = sum_t P'[h][t] * B[t][d], P' = p * s_t / 2^e (fp16) staged
-//       through a 1-2 KB LDS buffer; value codes get the same tr8 + OR
-//       treatment; the per-token zero points and 1024 offsets fold into a
-//       per-head bias subtracted from the accumulator at each page.
+//  PV   O[h][d] = sum_t P'[h][t] * B[t][d], P' = p * s_t (fp16) staged
+//       through a 1-2 KB LDS buffer; value codes get the same tr8 + mask
+//       treatment, so output tile a (channel slot a) accumulates 4^a O plus
+//       1024 sum_t P'; the per-token zero points and the 1024 offsets are
+//       subtracted from the accumulator at each page, and the 4^a is
+//       divided out when the split's partial is written.
 //
 // Reduction index k of every MFMA follows the natural channel / token order
-// within a 32-wide step; the mantissa position of a code (bit 0 or bit 8 of a
-// half) is the per-k power 2^e in {1, 256}, compensated in A.
+// within a 32-wide step (the tr8 row order puts even and odd bytes of a
+// word on consecutive k).
 #include "common.h"
 #include "decode.h"
 
@@ -56,31 +61,42 @@ __device__ __forceinline__ i32x2 tr8(const unsigned char *lds)
     return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2 *)lds);
 }
 
-// Slot `a` (token 4j+a of a key byte, or channel 4j+a of a value byte) of the
-// 8 transposed bytes -> 8 fp16 MFMA inputs: rows (0,1) at 1024 + c, rows
-// (2,3) at 1024 + 256 c, then rows (4,5), (6,7) likewise.
-// The three masks live in VGPRs (see CodeMasks) so each half pair is one
-// v_and_or_b32; gfx9 VOP3 cannot encode two literal operands.
+// Slot `a` (token 4j+a of a key byte, or channel 4j+a of a value byte) of
+// the 8 transposed bytes -> 8 fp16 MFMA inputs 1024 + 4^a c: the even bytes
+// of each word are masked in place, the odd bytes after the word was shifted
+// right by 8 (done once per word, shared by the four slots).  The masks live
+// in VGPRs (see CodeMasks) so each half pair is one v_and_or_b32; gfx9 VOP3
+// cannot encode two literal operands.
 struct CodeMasks {
-    unsigned lo, hi, one;  // 0x00030003, 0x03000300, 0x64006400
+    unsigned slot[4];  // 0x00030003 << 2a
+    unsigned one;      // 0x64006400
 };
 
 __device__ __forceinline__ CodeMasks code_masks()
 {
-    CodeMasks m{0x00030003u, 0x03000300u, 0x64006400u};
-    asm volatile("" : "+v"(m.lo), "+v"(m.hi), "+v"(m.one));
+    CodeMasks m{{0x00030003u, 0x000C000Cu, 0x00300030u, 0x00C000C0u}, 0x64006400u};
+    asm volatile("" : "+v"(m.slot[0]), "+v"(m.slot[1]), "+v"(m.slot[2]), "+v"(m.slot[3]), "+v"(m.one));
     return m;
 }
 
-template <int A>
-__device__ __forceinline__ half8 codes_to_half8(i32x2 raw, const CodeMasks &m)
+// A tr8 result and its odd bytes moved down: {w0, w1, w0 >> 8, w1 >> 8}.
+struct RawCodes {
+    unsigned w[4];
+};
+
+__device__ __forceinline__ RawCodes raw_codes(i32x2 raw)
 {
-    const unsigned w0 = (unsigned)raw[0] >> (2 * A), w1 = (unsigned)raw[1] >> (2 * A);
+    return RawCodes{{(unsigned)raw[0], (unsigned)raw[1], (unsigned)raw[0] >> 8, (unsigned)raw[1] >> 8}};
+}
+
+template <int A>
+__device__ __forceinline__ half8 codes_to_half8(const RawCodes &r, const CodeMasks &m)
+{
     u32x4 v;
-    v[0] = (w0 & m.lo) | m.one;
-    v[1] = (w0 & m.hi) | m.one;
-    v[2] = (w1 & m.lo) | m.one;
-    v[3] = (w1 & m.hi) | m.one;
+    v[0] = (r.w[0] & m.slot[A]) | m.one;
+    v[1] = (r.w[2] & m.slot[A]) | m.one;
+    v[2] = (r.w[1] & m.slot[A]) | m.one;
+    v[3] = (r.w[3] & m.slot[A]) | m.one;
     return __builtin_bit_cast(half8, v);
 }
 
@@ -298,12 +314,7 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     constexpr int HPL = GQ / 4;
     constexpr int RSTEP = 4 / HPL;  // accumulator register of head slot j = j * RSTEP
     const int q = lane >> 4, r = lane & 15;
-    const half8 bw_hi = __builtin_bit_cast(half8, u32x4{0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u});
-    const half2v neg1024 = as_h2(0xE400E400u);
-    const half2v negs_lo = as_h2(0xBC00BC00u);   // -1
-    const half2v negs_hi = as_h2(0xDC00DC00u);   // -256
-    const half2v one1024 = as_h2(0x64006400u);
-    const half2v s256 = as_h2(0x5C005C00u);      // 256
+    const half8 neg1024 = __builtin_bit_cast(half8, u32x4{0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u});
 
     const CodeMasks cm = code_masks();
 
@@ -329,19 +340,21 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
             ksh[i] = *(const _Float16 *)(st + kMeta + 2 * W.hch[i]);
     }
 
-    // ---------------- QK A operands and bias tile
+    // ---------------- QK A operands and the bias tiles X = -1024 sum A,
+    // Y = -sum A z (per head row, broadcast over token columns)
     half8 A[4], Ahi;
-    f32x4 bias = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 Xt = {0.0f, 0.0f, 0.0f, 0.0f}, Yt = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        u32x4 av, bw;
+        u32x4 av, nz;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             av[j] = as_u(as_h2(W.qv[s][j]) * as_h2(ks[s][j]));
-            bw[j] = as_u(__builtin_elementwise_fma(as_h2(kz[s][j]), (j & 1) ? negs_hi : negs_lo, neg1024));
+            nz[j] = kz[s][j] ^ 0x80008000u;
         }
         A[s] = __builtin_bit_cast(half8, av);
-        bias = mfma(A[s], __builtin_bit_cast(half8, bw), bias);
+        Xt = mfma(A[s], neg1024, Xt);
+        Yt = mfma(A[s], __builtin_bit_cast(half8, nz), Yt);
     }
     if (Dk > 0) {
         u32x4 av;
@@ -353,32 +366,36 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
             av[j] = as_u(as_h2(W.qvh[j]) * h);
         }
         Ahi = __builtin_bit_cast(half8, av);
-        bias = mfma(Ahi, bw_hi, bias);
+        Xt = mfma(Ahi, neg1024, Xt);
     }
 
     // ---------------- QK token tiles: S[cb][a] covers tokens 64cb + 4r + a
+    // and holds 4^a (S - bias) after the MFMAs below.
     f32x4 S[2][4];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-            S[cb][a] = bias;
+    for (int a = 0; a < 4; ++a) {
+        const f32x4 init = Xt + Yt * (float)(1 << (2 * a));
+        S[0][a] = init;
+        S[1][a] = init;
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-            S[cb][0] = mfma(A[s], codes_to_half8<0>(kraw[s][cb], cm), S[cb][0]);
-            S[cb][1] = mfma(A[s], codes_to_half8<1>(kraw[s][cb], cm), S[cb][1]);
-            S[cb][2] = mfma(A[s], codes_to_half8<2>(kraw[s][cb], cm), S[cb][2]);
-            S[cb][3] = mfma(A[s], codes_to_half8<3>(kraw[s][cb], cm), S[cb][3]);
+            const RawCodes rc = raw_codes(kraw[s][cb]);
+            S[cb][0] = mfma(A[s], codes_to_half8<0>(rc, cm), S[cb][0]);
+            S[cb][1] = mfma(A[s], codes_to_half8<1>(rc, cm), S[cb][1]);
+            S[cb][2] = mfma(A[s], codes_to_half8<2>(rc, cm), S[cb][2]);
+            S[cb][3] = mfma(A[s], codes_to_half8<3>(rc, cm), S[cb][3]);
         }
     if (Dk > 0) {
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-            S[cb][0] = mfma(Ahi, codes_to_half8<0>(hraw[cb], cm), S[cb][0]);
-            S[cb][1] = mfma(Ahi, codes_to_half8<1>(hraw[cb], cm), S[cb][1]);
-            S[cb][2] = mfma(Ahi, codes_to_half8<2>(hraw[cb], cm), S[cb][2]);
-            S[cb][3] = mfma(Ahi, codes_to_half8<3>(hraw[cb], cm), S[cb][3]);
+            const RawCodes rc = raw_codes(hraw[cb]);
+            S[cb][0] = mfma(Ahi, codes_to_half8<0>(rc, cm), S[cb][0]);
+            S[cb][1] = mfma(Ahi, codes_to_half8<1>(rc, cm), S[cb][1]);
+            S[cb][2] = mfma(Ahi, codes_to_half8<2>(rc, cm), S[cb][2]);
+            S[cb][3] = mfma(Ahi, codes_to_half8<3>(rc, cm), S[cb][3]);
         }
     }
 
@@ -390,36 +407,42 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
         vraw[s][1] = tr8(st + kVal + 1024 * s + W.tr_base1);
     }
 
-    // ---------------- online softmax and P' (fp16) with the PV bias.
+    // ---------------- online softmax and P' = p * s_t (fp16) with the PV bias.
     // P' goes to the key-low region of this stage, whose codes are consumed.
     _Float16 *pbuf = (_Float16 *)(st + kKlo);
     const u32x4 vm0 = *(const u32x4 *)(st + kMeta + 512 + 4 * (4 * r));
     const u32x4 vm1 = *(const u32x4 *)(st + kMeta + 512 + 4 * (64 + 4 * r));
-    float alpha[HPL], vbias[HPL];
+    const half2v ones = as_h2(0x3C003C00u);
+    float alpha[HPL], xv[HPL], yv[HPL];
 #pragma unroll
     for (int j = 0; j < HPL; ++j) {
         const int ri = j * RSTEP;
-        float mx = S[0][0][ri];
+        float sv[2][4];
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
             for (int a = 0; a < 4; ++a)
-                mx = fmaxf(mx, S[cb][a][ri]);
+                sv[cb][a] = S[cb][a][ri] * (1.0f / (float)(1 << (2 * a)));
+        float mx = sv[0][0];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+                mx = fmaxf(mx, sv[cb][a]);
         mx = row_max16(mx);
         const float mn = fmaxf(W.m_run[j], mx);
         alpha[j] = __builtin_amdgcn_exp2f(W.m_run[j] - mn);
         W.m_run[j] = mn;
-        float lsum = 0.0f, lsum256 = 0.0f, bsum = 0.0f;
+        float lsum = 0.0f, xsum = 0.0f, ysum = 0.0f;
         const int h = q * HPL + j;
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
             const u32x4 vm = cb ? vm1 : vm0;
-            const float p0v = __builtin_amdgcn_exp2f(S[cb][0][ri] - mn);
-            const float p1v = __builtin_amdgcn_exp2f(S[cb][1][ri] - mn);
-            const float p2v = __builtin_amdgcn_exp2f(S[cb][2][ri] - mn - 8.0f);  // p / 256
-            const float p3v = __builtin_amdgcn_exp2f(S[cb][3][ri] - mn - 8.0f);
-            lsum += p0v + p1v;
-            lsum256 += p2v + p3v;
+            const float p0v = __builtin_amdgcn_exp2f(sv[cb][0] - mn);
+            const float p1v = __builtin_amdgcn_exp2f(sv[cb][1] - mn);
+            const float p2v = __builtin_amdgcn_exp2f(sv[cb][2] - mn);
+            const float p3v = __builtin_amdgcn_exp2f(sv[cb][3] - mn);
+            lsum += (p0v + p1v) + (p2v + p3v);
             // (scale, zero) pairs of tokens 64cb + 4r + {0..3}
             const half2v sv01 = as_h2(__builtin_amdgcn_perm(vm[1], vm[0], 0x05040100u));
             const half2v zv01 = as_h2(__builtin_amdgcn_perm(vm[1], vm[0], 0x07060302u));
@@ -427,24 +450,26 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
             const half2v zv23 = as_h2(__builtin_amdgcn_perm(vm[3], vm[2], 0x07060302u));
             const half2v a01 = as_h2(pack_h2(p0v, p1v)) * sv01;
             const half2v a23 = as_h2(pack_h2(p2v, p3v)) * sv23;
-            const half2v w01 = zv01 + one1024;
-            const half2v w23 = __builtin_elementwise_fma(zv23, s256, one1024);
-            bsum = __builtin_amdgcn_fdot2(a01, w01, bsum, false);
-            bsum = __builtin_amdgcn_fdot2(a23, w23, bsum, false);
+            xsum = __builtin_amdgcn_fdot2(a01, ones, xsum, false);
+            xsum = __builtin_amdgcn_fdot2(a23, ones, xsum, false);
+            ysum = __builtin_amdgcn_fdot2(a01, zv01, ysum, false);
+            ysum = __builtin_amdgcn_fdot2(a23, zv23, ysum, false);
             *(uint2 *)(pbuf + h * 128 + 64 * cb + 4 * r) = make_uint2(as_u(a01), as_u(a23));
         }
-        W.l_run[j] = W.l_run[j] * alpha[j] + lsum + 256.0f * lsum256;
-        vbias[j] = row_sum16(bsum);
+        W.l_run[j] = W.l_run[j] * alpha[j] + lsum;
+        xv[j] = 1024.0f * row_sum16(xsum);
+        yv[j] = row_sum16(ysum);
     }
 
-    // ---------------- PV: O = O * alpha - bias + P' V
+    // ---------------- PV: O_a = O_a * alpha - (1024 sum P' + 4^a sum P' z) + P' V
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
             for (int j = 0; j < HPL; ++j)
-                W.O[cb][a][j * RSTEP] = W.O[cb][a][j * RSTEP] * alpha[j] - vbias[j];
+                W.O[cb][a][j * RSTEP] =
+                    W.O[cb][a][j * RSTEP] * alpha[j] - (xv[j] + yv[j] * (float)(1 << (2 * a)));
     // P' rows are read with inline asm: the compiler cannot tell this stage
     // apart from the one the next page is streaming into and would otherwise
     // wait for that prefetch (vmcnt(0)) here.  LDS executes a wave's
@@ -466,10 +491,11 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-            W.O[cb][0] = mfma(Ap[s], codes_to_half8<0>(vraw[s][cb], cm), W.O[cb][0]);
-            W.O[cb][1] = mfma(Ap[s], codes_to_half8<1>(vraw[s][cb], cm), W.O[cb][1]);
-            W.O[cb][2] = mfma(Ap[s], codes_to_half8<2>(vraw[s][cb], cm), W.O[cb][2]);
-            W.O[cb][3] = mfma(Ap[s], codes_to_half8<3>(vraw[s][cb], cm), W.O[cb][3]);
+            const RawCodes rc = raw_codes(vraw[s][cb]);
+            W.O[cb][0] = mfma(Ap[s], codes_to_half8<0>(rc, cm), W.O[cb][0]);
+            W.O[cb][1] = mfma(Ap[s], codes_to_half8<1>(rc, cm), W.O[cb][1]);
+            W.O[cb][2] = mfma(Ap[s], codes_to_half8<2>(rc, cm), W.O[cb][2]);
+            W.O[cb][3] = mfma(Ap[s], codes_to_half8<3>(rc, cm), W.O[cb][3]);
         }
 }
 
@@ -550,12 +576,11 @@ void decode_mfma_kernel(DecodeParams p)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const half2v h = as_h2(qraw[s][j]);
-                const float inv = (j & 1) ? qscale * (1.0f / 256.0f) : qscale;
-                W.qv[s][j] = pack_h2((float)h[0] * inv, (float)h[1] * inv);
+                W.qv[s][j] = pack_h2((float)h[0] * qscale, (float)h[1] * qscale);
             }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float inv = (j & 1) ? qscale * (4.0f / 256.0f) : qscale * 4.0f;
+            const float inv = qscale * 4.0f;  // high bits weigh 4
             const int r0 = 8 * q + 2 * j;
             W.qvh[j] = pack_h2(r0 < Dk ? (float)qh[2 * j] * inv : 0.0f,
                                r0 + 1 < Dk ? (float)qh[2 * j + 1] * inv : 0.0f);
@@ -649,8 +674,9 @@ void decode_mfma_kernel(DecodeParams p)
         float *o = p.ws_o + row * 128;
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-            float4 v = make_float4(W.O[cb][0][j * RSTEP], W.O[cb][1][j * RSTEP], W.O[cb][2][j * RSTEP],
-                                   W.O[cb][3][j * RSTEP]);
+            // output tile a holds 4^a O for channels 64cb + 4r + a
+            float4 v = make_float4(W.O[cb][0][j * RSTEP], W.O[cb][1][j * RSTEP] * 0.25f,
+                                   W.O[cb][2][j * RSTEP] * 0.0625f, W.O[cb][3][j * RSTEP] * 0.015625f);
             if (poison)
                 v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
             *(float4 *)(o + 64 * cb + 4 * r) = v;
