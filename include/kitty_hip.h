@@ -200,6 +200,36 @@ int kitty_paged_decode(const kitty_decode_args *args, kitty_stream_t stream);
 int kitty_paged_decode_splits(const kitty_decode_args *args, kitty_stream_t stream);
 int kitty_paged_decode_merge(const kitty_decode_args *args, kitty_stream_t stream);
 
+/* ------------------------------------------------------ token append
+ * Replaces the FP16 buffer writes of KittyInferencePipeline.push_token
+ * (kitty/pipeline.py:115-181) for B sequences in one launch: sequence b's
+ * new key / value (H x D) goes to row sink_fill[slot] of its sink buffer
+ * while sink_fill[slot] < sink_size, else to row buf_len[slot] of its key /
+ * value buffer, and that counter is incremented on the device.  A sequence
+ * whose buffer already holds buf_tokens tokens (the caller did not spill it
+ * with kitty_quantize_kv_blocks) is left unchanged and overflow[b] is set to
+ * 1.  Slots must be distinct within one call.  Buffers and key / value rows
+ * must be 16-byte aligned, head_dim a multiple of 8. */
+typedef struct {
+    int64_t s_slot, s_head, s_tok; /* element strides; the channel stride is 1 */
+} kitty_slot_layout;
+
+typedef struct {
+    const uint16_t *key, *value; /* (B, H, D) fp16, the new token of every sequence */
+    int64_t key_s_seq, key_s_head, value_s_seq, value_s_head;
+    const int32_t *slots;        /* (B,) buffer slot of each sequence */
+    uint16_t *sink_k, *sink_v;   /* (num_slots, H, sink_size, D) of this layer */
+    kitty_slot_layout sink_layout;
+    uint16_t *buf_k, *buf_v;     /* (num_slots, H, buf_tokens, D) of this layer */
+    kitty_slot_layout buf_layout;
+    int32_t *sink_fill;          /* (num_slots,) tokens in each sink buffer */
+    int32_t *buf_len;            /* (num_slots,) tokens in each key / value buffer */
+    int32_t *overflow;           /* (B,) */
+    int32_t batch, num_kv_heads, head_dim, sink_size, buf_tokens, num_slots;
+} kitty_append_args;
+
+int kitty_append_tokens(const kitty_append_args *args, kitty_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -79,11 +79,29 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class SlotLayout(ctypes.Structure):
+    _fields_ = [("s_slot", _i64), ("s_head", _i64), ("s_tok", _i64)]
+
+
+class AppendArgs(ctypes.Structure):
+    """kitty_append_args: one token for each of B sequences into its FP16 buffers."""
+    _fields_ = [
+        ("key", _vp), ("value", _vp),
+        ("key_s_seq", _i64), ("key_s_head", _i64), ("value_s_seq", _i64), ("value_s_head", _i64),
+        ("slots", _vp),
+        ("sink_k", _vp), ("sink_v", _vp), ("sink_layout", SlotLayout),
+        ("buf_k", _vp), ("buf_v", _vp), ("buf_layout", SlotLayout),
+        ("sink_fill", _vp), ("buf_len", _vp), ("overflow", _vp),
+        ("batch", _i32), ("num_kv_heads", _i32), ("head_dim", _i32), ("sink_size", _i32), ("buf_tokens", _i32),
+        ("num_slots", _i32),
+    ]
+
+
 EXPORTED_SYMBOLS = (
     "kitty_abi_version", "kitty_last_error", "kitty_quantize_kv_blocks",
     "kitty_dequantize_key_page", "kitty_dequantize_value_page",
     "kitty_decode_workspace_size", "kitty_paged_decode", "kitty_paged_decode_splits",
-    "kitty_paged_decode_merge",
+    "kitty_paged_decode_merge", "kitty_append_tokens",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -112,6 +130,7 @@ def load() -> ctypes.CDLL:
     L.kitty_paged_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_paged_decode_splits.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_paged_decode_merge.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
+    L.kitty_append_tokens.argtypes = [ctypes.POINTER(AppendArgs), _vp]
     if L.kitty_abi_version() != KITTY_ABI_VERSION:
         raise ImportError(f"libkitty_hip ABI {L.kitty_abi_version()} != {KITTY_ABI_VERSION}")
     _lib = L

@@ -10,9 +10,12 @@ batch-quantize launch for every sequence whose buffer fills), then one fused
 split-K paged decode attends sinks, pages and the FP16 tail of every
 sequence at once.
 
-Prefill (T > 1): tokens are pushed one position at a time for the whole
-batch, and the output is causal attention over the chunk, as the reference
-computes it (``:153-191``); it runs in float32 (torch's SDPA math path).
+Prefill (T > 1): the chunk goes into the pipeline in bulk (sinks and buffer
+rows copied, every complete page quantised straight from the chunk in one
+launch per sequence; the same state as pushing the tokens one at a time,
+which is what the reference does, ``:169-177``), and the output is causal
+attention over the chunk, as the reference computes it (``:179-191``); it
+runs in float32 (torch's SDPA math path).
 """
 from __future__ import annotations
 
@@ -74,9 +77,7 @@ class KittyPagedAttention(nn.Module):
         return plan.run().unsqueeze(2).to(q.dtype)
 
     def _prefill(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids: List[int]) -> torch.Tensor:
-        T = q.shape[2]
-        for t in range(T):
-            self.pipeline.push_tokens(self.layer_id, k[:, :, t], v[:, :, t], seq_ids)
+        self.pipeline.push_chunk(self.layer_id, k, v, seq_ids)
         k_exp = k.float().repeat_interleave(self.q_per_kv, dim=1)
         v_exp = v.float().repeat_interleave(self.q_per_kv, dim=1)
         out = F.scaled_dot_product_attention(q.float(), k_exp, v_exp, attn_mask=None, dropout_p=0.0,

@@ -35,19 +35,27 @@ def outlier_keys(gen: torch.Generator, shape, H: int, D: int, n_outlier: int, fa
     return k.half(), channels
 
 
-def random_pools(gen: torch.Generator, P: int, H: int, D: int, G: int, d_boost: int, bi: torch.Tensor):
+def random_pools(gen: torch.Generator, P: int, H: int, D: int, G: int, d_boost: int, bi: torch.Tensor,
+                 rng: np.random.Generator = None):
     """Pools filled with arbitrary valid encodings: random code bytes, positive
     fp16 scales and integer zero points within each channel's code range.
     Every byte pattern is a valid packed page, so this exercises the decode
-    path on all code values without running a quantiser."""
+    path on all code values without running a quantiser.  With `rng`, the
+    code bytes come from numpy (much faster for GB-sized pools)."""
     sentinel = min(d_boost + 1, 255)
-    kb = torch.randint(0, 256, (P, H, D, G // 4), generator=gen, dtype=torch.uint8)
-    kh = torch.randint(0, 256, (P, H, d_boost, G // 4), generator=gen, dtype=torch.uint8)
+
+    def code_bytes(shape):
+        if rng is not None:
+            return torch.from_numpy(rng.integers(0, 256, size=shape, dtype=np.uint8))
+        return torch.randint(0, 256, shape, generator=gen, dtype=torch.uint8)
+
+    kb = code_bytes((P, H, D, G // 4))
+    kh = code_bytes((P, H, d_boost, G // 4))
     mq = torch.where(bi < sentinel, 15, 3).float()              # (H, D)
     ks = (torch.rand(P, H, D, generator=gen) * 0.6 + 0.05)
     kz = torch.floor(torch.rand(P, H, D, generator=gen) * (mq + 1)).clamp(max=mq)
     km = torch.stack([ks, kz], dim=2).half()
-    vp = torch.randint(0, 256, (P, H, G, D // 4), generator=gen, dtype=torch.uint8)
+    vp = code_bytes((P, H, G, D // 4))
     vs = torch.rand(P, H, G, generator=gen) * 0.6 + 0.3
     vz = torch.floor(torch.rand(P, H, G, generator=gen) * 4).clamp(max=3)
     vm = torch.stack([vs, vz], dim=3).half()

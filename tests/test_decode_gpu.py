@@ -153,3 +153,53 @@ def test_invalid_page_id_poisons_output(dev):
     out = _run_batched(dev, c)
     assert np.isnan(out[1]).all()
     _close(out[0], _oracle_batched(c, Hq, H, D, 0), "b=0")
+
+
+def test_config4_ragged_batch_64bit_offsets(dev):
+    """BASELINE config 4 at full size: 64 sequences with seeded ragged
+    contexts in [512, 65536], 32 query / 8 KV heads, 25% INT4 channels
+    (D_boost = 32), pages scattered by a shuffled free list over a
+    70,000-page pool, so page ids beyond 65,536 put key / value byte offsets
+    past 2^31 (64-bit addressing).  Every sequence and head against the oracle."""
+    from kitty.kernels import paged_attention_batched
+    B, Hq, H, D, G, dk, S = 64, 32, 8, 128, 128, 32, 32
+    P_dev = 70_000
+    ctx = [int(x) for x in ragged_lengths(4, B, 512, 65536)]
+    n_pages = [(c - S) // G for c in ctx]
+    tails = [(c - S) % G for c in ctx]
+    U = sum(n_pages)
+    gen = torch.Generator().manual_seed(44)
+    bi = torch.full((H, D), dk + 1, dtype=torch.uint8)
+    for h in range(H):
+        bi[h, torch.randperm(D, generator=gen)[:dk]] = torch.arange(dk, dtype=torch.uint8)
+    host = random_pools(gen, U, H, D, G, dk, bi, rng=np.random.default_rng(44))  # compact: list page u = row u
+    ids = torch.randperm(P_dev, generator=gen)[:U]               # shuffled free list
+    assert int(ids.max()) >= 65_536                              # some byte offsets exceed 2^31
+    shapes = [(P_dev,) + tuple(t.shape[1:]) for t in host]
+    pools = [torch.empty(s, dtype=t.dtype, device=dev) for s, t in zip(shapes, host)]
+    ids_dev = ids.to(dev)
+    for pd, t in zip(pools, host):
+        pd.index_copy_(0, ids_dev, t.to(dev))
+    W = max(n_pages)
+    bt = torch.zeros(B, W, dtype=torch.int32)
+    bt_compact = torch.zeros(B, W, dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        bt[b, :n_pages[b]] = ids[off:off + n_pages[b]].to(torch.int32)
+        bt_compact[b, :n_pages[b]] = torch.arange(off, off + n_pages[b], dtype=torch.int32)
+        off += n_pages[b]
+    T = max(tails)
+    q = torch.randn(B, Hq, D, generator=gen).half()
+    sk, sv = torch.randn(B, H, S, D, generator=gen).half(), torch.randn(B, H, S, D, generator=gen).half()
+    tk, tv = torch.randn(B, H, T, D, generator=gen).half(), torch.randn(B, H, T, D, generator=gen).half()
+    out = paged_attention_batched(
+        q.to(dev), bt.to(dev), torch.tensor(n_pages, dtype=torch.int32, device=dev), *pools, bi.to(dev),
+        sk.to(dev), sv.to(dev), torch.full((B,), S, dtype=torch.int32, device=dev), tk.to(dev), tv.to(dev),
+        torch.tensor(tails, dtype=torch.int32, device=dev)).cpu().numpy()
+    del pools
+    kb, kh, km, vp, vm = [t.numpy() for t in host]
+    for b in range(B):
+        n, t = n_pages[b], tails[b]
+        ref = O.paged_attention(q[b].numpy(), bt_compact[b, :n].numpy(), kb, kh, km, vp, vm, bi.numpy(), dk,
+                                sk[b].numpy(), sv[b].numpy(), tk[b, :, :t].numpy(), tv[b, :, :t].numpy(), Hq, H, D)
+        _close(out[b], ref, f"config4 b={b} ctx={ctx[b]}")

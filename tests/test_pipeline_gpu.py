@@ -209,3 +209,55 @@ def test_prefill_output_is_causal_attention(dev):
     ref = torch.softmax(s, -1) @ ve
     assert torch.allclose(out, ref, atol=2e-3, rtol=1e-2)
     assert len(layout.get_page_list(0, 0)) == (21 - 4) // 8 and pipe.key_qbuf_len == (21 - 4) % 8
+
+
+def _logical_pages(p, lay, seq, layer):
+    """Page bytes of a sequence in logical order, from the five pools."""
+    out = []
+    for phys in lay.get_page_list(seq, layer):
+        out.append(tuple(t[phys].cpu() for t in (lay.key_baseline, lay.key_boost, lay.key_metadata,
+                                                  lay.value_pool, lay.value_metadata)))
+    return out
+
+
+@pytest.mark.parametrize("D,G,S,pre,T", [(16, 8, 4, 0, 61), (16, 8, 4, 6, 50), (128, 128, 32, 0, 700),
+                                         (128, 128, 32, 45, 400)])
+def test_bulk_prefill_matches_token_pushes(dev, D, G, S, pre, T):
+    """push_chunk (bulk prefill: sinks and buffer rows copied, complete pages
+    quantised straight from the chunk) leaves exactly the state of T single
+    pushes: same sinks, buffers, counters (host and device), page bytes."""
+    cfg = _cfg(num_layers=2, num_kv_heads=2, head_dim=D, q_buffer_size=G, sink_size=S, local_value_window=G,
+               boost_rate=0.125, max_batch_size=2)
+    gen = torch.Generator().manual_seed(D + T)
+    B, H = 2, cfg.num_kv_heads
+    K = torch.randn(B, H, pre + T, D, generator=gen).half().to(dev)
+    V = torch.randn(B, H, pre + T, D, generator=gen).half().to(dev)
+    a, lay_a, _ = _pipe(cfg)
+    b, lay_b, _ = _pipe(cfg)
+    for layer in range(2):
+        for t in range(pre):
+            a.push_tokens(layer, K[:, :, t], V[:, :, t], [0, 1])
+            b.push_tokens(layer, K[:, :, t], V[:, :, t], [0, 1])
+        for t in range(pre, pre + T):
+            a.push_tokens(layer, K[:, :, t], V[:, :, t], [0, 1])
+        b.push_chunk(layer, K[:, :, pre:], V[:, :, pre:], [0, 1])
+    torch.cuda.synchronize()
+    assert np.array_equal(a._fill, b._fill) and np.array_equal(a._qlen, b._qlen)
+    assert np.array_equal(a._npages, b._npages)
+    assert torch.equal(a.lens, b.lens)
+    assert np.array_equal(a.lens[0].cpu().numpy().T, a._fill)
+    assert np.array_equal(a.lens[1].cpu().numpy().T, a._qlen)
+    assert np.array_equal(a.lens[2].cpu().numpy().T, a._npages)
+    for layer in range(2):
+        for seq in range(B):
+            s = a.slot(seq)
+            f, q = int(a._fill[s, layer]), int(a._qlen[s, layer])
+            assert torch.equal(a._sink_k[s, layer, :, :f], b._sink_k[s, layer, :, :f])
+            assert torch.equal(a._sink_v[s, layer, :, :f], b._sink_v[s, layer, :, :f])
+            assert torch.equal(a._qbuf_k[s, layer, :, :q], b._qbuf_k[s, layer, :, :q])
+            assert torch.equal(a._qbuf_v[s, layer, :, :q], b._qbuf_v[s, layer, :, :q])
+            pa, pb = _logical_pages(a, lay_a, seq, layer), _logical_pages(b, lay_b, seq, layer)
+            assert len(pa) == len(pb) == int(a._npages[s, layer])
+            for x, y in zip(pa, pb):
+                assert all(torch.equal(u, v) for u, v in zip(x, y))
+    assert not a.overflowed() and not b.overflowed()
