@@ -230,6 +230,16 @@ typedef struct {
 
 int kitty_append_tokens(const kitty_append_args *args, kitty_stream_t stream);
 
+/* ------------------------------------------- sensitivity accumulation
+ * Replaces _ChannelAccumulator.update (kitty/sensitivity.py:46-61):
+ * out[h*head_dim + d] += sum over b < batch, t < tokens of
+ * |key[b*s_b + t*s_t + h*s_h + d]| in fp32, key fp16 with a contiguous
+ * channel dimension (the hook's (B, H, T, D) view of a key projection).
+ * The summation order is fixed, so repeated runs give identical sums. */
+int kitty_channel_abs_sum(const uint16_t *key, int64_t s_b, int64_t s_t, int64_t s_h, int32_t batch,
+                          int32_t tokens, int32_t num_kv_heads, int32_t head_dim, float *out,
+                          kitty_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

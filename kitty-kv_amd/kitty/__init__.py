@@ -8,6 +8,7 @@ from .config import KittyConfig
 from .layout import Page, PageCentricKVLayoutManager
 from .pipeline import KittyInferencePipeline
 from .attention import KittyPagedAttention, KittyAttentionFactory
+from .sensitivity import KittySensitivityProfiler
 
 __version__ = "0.1.0"
 __description__ = (
@@ -21,4 +22,5 @@ __all__ = [
     "KittyInferencePipeline",
     "KittyPagedAttention",
     "KittyAttentionFactory",
+    "KittySensitivityProfiler",
 ]

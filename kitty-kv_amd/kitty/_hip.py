@@ -101,7 +101,7 @@ EXPORTED_SYMBOLS = (
     "kitty_abi_version", "kitty_last_error", "kitty_quantize_kv_blocks",
     "kitty_dequantize_key_page", "kitty_dequantize_value_page",
     "kitty_decode_workspace_size", "kitty_paged_decode", "kitty_paged_decode_splits",
-    "kitty_paged_decode_merge", "kitty_append_tokens",
+    "kitty_paged_decode_merge", "kitty_append_tokens", "kitty_channel_abs_sum",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -131,6 +131,7 @@ def load() -> ctypes.CDLL:
     L.kitty_paged_decode_splits.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_paged_decode_merge.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_append_tokens.argtypes = [ctypes.POINTER(AppendArgs), _vp]
+    L.kitty_channel_abs_sum.argtypes = [_vp, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _vp]
     if L.kitty_abi_version() != KITTY_ABI_VERSION:
         raise ImportError(f"libkitty_hip ABI {L.kitty_abi_version()} != {KITTY_ABI_VERSION}")
     _lib = L

@@ -1,0 +1,114 @@
+"""Channel-sensitivity profiler (reference kitty/sensitivity.py): ranking,
+on-disk formats, and the device accumulation kernel."""
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from kitty import KittyConfig, KittySensitivityProfiler
+from kitty.sensitivity import rank_channels
+
+
+def test_rank_channels_known_answer():
+    scores = torch.tensor([[[0.1, 5.0, 3.0, 5.0, 0.2, 4.0, 1.0, 2.0]]])   # (1, 1, 8); channels 1 and 3 tie
+    masks, idx = rank_channels(scores, 3, 4)
+    assert idx[0, 0].tolist() == [4, 0, 4, 1, 4, 2, 4, 4]                 # ties rank by channel index
+    assert masks[0, 0].tolist() == [False, True, False, True, False, True, False, False]
+    _, idx0 = rank_channels(scores, 0, 1)
+    assert (idx0 == 1).all()
+
+
+def test_rank_channels_matches_topk_without_ties():
+    g = torch.Generator().manual_seed(1)
+    scores = torch.rand(3, 4, 128, generator=g)
+    masks, idx = rank_channels(scores, 16, 17)
+    top = scores.topk(16, dim=-1).indices                                  # sensitivity.py:191-193
+    ref = torch.zeros_like(masks).scatter_(-1, top, True)
+    assert torch.equal(masks, ref)
+    order = scores.argsort(dim=-1, descending=True)
+    for r in range(16):                                                    # :197-203
+        assert (idx.gather(-1, order[..., r:r + 1]) == r).all()
+
+
+def test_save_load_formats(tmp_path):
+    cfg = KittyConfig(num_layers=2, num_kv_heads=2, head_dim=16, boost_rate=0.25, device="cpu")
+    prof = KittySensitivityProfiler(cfg)
+    prof.scores_ = torch.rand(2, 2, 16, generator=torch.Generator().manual_seed(2))
+    prof.boost_masks_, prof.boost_idx_uint8_ = rank_channels(prof.scores_, cfg.d_boost, cfg.sentinel)
+    prof.save(tmp_path)
+    for name, dtype in (("scores.pt", torch.float32), ("boost_masks.pt", torch.bool), ("boost_idx.pt", torch.uint8)):
+        t = torch.load(tmp_path / name, weights_only=True)
+        assert t.dtype == dtype and tuple(t.shape) == (2, 2, 16)
+    meta = json.load(open(tmp_path / "meta.json"))
+    assert meta["d_boost"] == cfg.d_boost and meta["head_dim"] == 16 and "token_count" in meta
+    back = KittySensitivityProfiler.load(tmp_path, cfg)
+    assert torch.equal(back.boost_idx_uint8, prof.boost_idx_uint8) and torch.equal(back.scores_, prof.scores_)
+
+
+def test_accumulation_needs_a_rocm_device():
+    cfg = KittyConfig(num_layers=1, num_kv_heads=2, head_dim=16, device="cpu")
+    prof = KittySensitivityProfiler(cfg)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        prof.update(0, torch.zeros(1, 2, 4, 16, dtype=torch.float16))
+
+
+@pytest.mark.gpu
+def test_abs_sum_kernel_matches_float64(dev):
+    cfg = KittyConfig(num_layers=1, num_kv_heads=4, head_dim=128, device="cuda:0")
+    g = torch.Generator().manual_seed(3)
+    raw = torch.randn(3, 777, 4 * 128, generator=g)
+    raw[..., 5] *= 8
+    out = raw.half().to(dev)
+    key = out.reshape(3, 777, 4, 128).permute(0, 2, 1, 3)                  # the hook's strided view
+    prof = KittySensitivityProfiler(cfg)
+    prof.update(0, key)
+    prof.update(0, key[:1])
+    acc = prof.accumulator(0)
+    ref = np.abs(out.reshape(3, 777, 4, 128).cpu().double().numpy()).sum(axis=(0, 1))
+    ref += np.abs(out[:1].reshape(1, 777, 4, 128).cpu().double().numpy()).sum(axis=(0, 1))
+    np.testing.assert_allclose(acc.sum_abs.cpu().numpy(), ref, rtol=1e-5)
+    assert acc.token_count == 4 * 777
+    again = KittySensitivityProfiler(cfg)
+    again.update(0, key)
+    again.update(0, key[:1])
+    assert torch.equal(again.accumulator(0).sum_abs, acc.sum_abs)          # fixed summation order
+
+
+@pytest.mark.gpu
+def test_hooks_on_key_projections(dev):
+    H, D, L = 2, 64, 2
+
+    class Attn(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.k_proj = torch.nn.Linear(32, H * D, bias=False)
+
+    class Layer(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.self_attn = Attn()
+
+    class Model(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.layers = torch.nn.ModuleList([Layer() for _ in range(L)])
+
+        def forward(self, x):
+            return [layer.self_attn.k_proj(x) for layer in self.layers]
+
+    torch.manual_seed(4)
+    model = Model().half().to(dev)
+    cfg = KittyConfig(num_layers=L, num_kv_heads=H, head_dim=D, boost_rate=0.125, device="cuda:0")
+    prof = KittySensitivityProfiler(cfg, model)
+    prof.register_hooks(range(L))
+    xs = [torch.randn(2, 50, 32, device=dev).half() for _ in range(3)]
+    outs = [model(x) for x in xs]
+    prof.remove_hooks()
+    prof.compute()
+    for l in range(L):
+        k = torch.cat([o[l].float().reshape(-1, H, D) for o in outs])
+        ref = k.abs().mean(0).cpu()
+        torch.testing.assert_close(prof.scores_[l], ref, rtol=1e-4, atol=1e-6)
+    _, want = rank_channels(prof.scores_, cfg.d_boost, cfg.sentinel)
+    assert torch.equal(prof.boost_idx_uint8, want)
