@@ -41,7 +41,7 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_workload(torch, dev, cfg, copies: int):
+def build_workload(torch, dev, cfg, copies: int, placement_kind: str = "shuffled"):
     from kitty.kernels.ops import DecodePlan, pool_store, quantize_into_pools
     B, Hq, Hkv, ctx = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["ctx"]
     dk = round(cfg["boost"] * D)
@@ -68,7 +68,10 @@ def build_workload(torch, dev, cfg, copies: int):
     vp = torch.empty(P, Hkv, G, D // 4, dtype=torch.uint8, device=dev)
     vm = torch.empty(P, Hkv, G, 2, dtype=torch.float16, device=dev)
     store = pool_store(kb, kh, km, vp, vm)
-    placement = torch.randperm(P, generator=gen)[:used].to(torch.int32)   # shuffled free list
+    if placement_kind == "shuffled":      # a fragmented pool: pages from a shuffled free list
+        placement = torch.randperm(P, generator=gen)[:used].to(torch.int32)
+    else:                                 # first-fit, B sequences growing in lockstep: page p of seq b
+        placement = torch.arange(used, dtype=torch.int32).view(copies, n_pages, B).transpose(1, 2).reshape(-1)
     g = torch.Generator(device=dev).manual_seed(cfg["seed"] + 100)
     scale = torch.ones(Hkv, D, device=dev)
     for h in range(Hkv):
@@ -203,6 +206,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", choices=sorted(CONFIGS), default="cfg3")
     ap.add_argument("--copies", type=int, default=3)
+    ap.add_argument("--placement", choices=["shuffled", "first-fit"], default="shuffled",
+                    help="page ids: a shuffled free list (fragmented pool) or first-fit order of B sequences "
+                         "growing in lockstep")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-quantize", action="store_true")
@@ -223,7 +229,7 @@ def main() -> int:
         return copy_probe(torch, dev)
     cfg = CONFIGS[args.config]
     log(f"building {args.config} workload ({args.copies} pool copies)")
-    w = build_workload(torch, dev, cfg, args.copies)
+    w = build_workload(torch, dev, cfg, args.copies, args.placement)
     nb = algorithmic_bytes(w)
     plans = w["plans"]
     log(f"pool {w['P']} pages, {nb['packed'] / 1e6:.1f} MB packed KV per step; warmup {args.warmup}")
