@@ -369,6 +369,10 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
         Xt = mfma(Ahi, neg1024, Xt);
     }
 
+    // The MFMA blocks run at raised wave priority: the other wave of the SIMD
+    // is then most often in its VALU / memory phase, and the matrix core
+    // stays fed (measured: 1.5-2 us less per launch at config 3).
+    __builtin_amdgcn_s_setprio(1);
     // ---------------- QK token tiles: S[cb][a] covers tokens 64cb + 4r + a
     // and holds 4^a (S - bias) after the MFMAs below.
     f32x4 S[2][4];
@@ -399,6 +403,7 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
         }
     }
 
+    __builtin_amdgcn_s_setprio(0);
     // value codes for PV, issued before the softmax so they arrive meanwhile
     i32x2 vraw[4][2];
 #pragma unroll
@@ -475,6 +480,7 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     // wait for that prefetch (vmcnt(0)) here.  LDS executes a wave's
     // operations in order, so the reads see the writes above; lgkmcnt(0)
     // makes their results available.
+    __builtin_amdgcn_s_setprio(1);
     half8 Ap[4];
     {
         const unsigned addr = (unsigned)(uintptr_t)(pbuf + W.prow * 128 + 8 * q);
@@ -497,6 +503,7 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
             W.O[cb][2] = mfma(Ap[s], codes_to_half8<2>(rc, cm), W.O[cb][2]);
             W.O[cb][3] = mfma(Ap[s], codes_to_half8<3>(rc, cm), W.O[cb][3]);
         }
+    __builtin_amdgcn_s_setprio(0);
 }
 
 // Occupancy target (waves per SIMD): two waves for GQA groups of 4 and 8
