@@ -265,12 +265,12 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
 
 // Combine the n_splits + 1 partials of (b, qh) and write the fp16 output.
 // One wave per (b, qh); each lane owns channels lane and lane + 64 (D <= 128
-// per pass).  Splits are taken 16 at a time with every load of a batch
+// per pass).  Splits are taken 32 at a time with every load of a batch
 // issued together, and merged with a running maximum, so a batch costs one
-// memory round trip.
+// memory round trip (config 3 has 17 partials per row: one batch).
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
 {
-    constexpr int kBatch = 16;
+    constexpr int kBatch = 32;
     const int lane = threadIdx.x;
     const int bq = blockIdx.x;
     const int b = bq / p.Hq, qh = bq - b * p.Hq;
@@ -287,8 +287,9 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
             for (int u = 0; u < kBatch; ++u) {
                 const bool ok = s0 + u < NS;
                 const int64_t row = row0 + (ok ? s0 + u : 0);
-                m[u] = ok ? p.ws_ml[2 * row] : ninf;
-                l[u] = ok ? p.ws_ml[2 * row + 1] : 0.0f;
+                const float2 ml = ok ? *(const float2 *)(p.ws_ml + 2 * row) : make_float2(ninf, 0.0f);
+                m[u] = ml.x;
+                l[u] = ml.y;
                 oa[u] = ok && da < p.D ? p.ws_o[row * p.D + da] : 0.0f;
                 ob[u] = ok && db < p.D ? p.ws_o[row * p.D + db] : 0.0f;
             }

@@ -13,11 +13,11 @@
 //       transposes the channel-major page in LDS so each lane holds 8
 //       channels of one byte column (4 tokens, one per slot a).
 //       A: q * scale_k[d] * log2(e)/sqrt(D) (fp16), heads on MFMA rows.
-//       Every MFMA of slot a accumulates 4^a S plus 1024 sum_k A[k]; the
-//       tile starts from -(1024 X + 4^a Y), X = sum_k A[k] and
-//       Y = sum_k A[k] z_k (two bias tiles, 9 MFMAs), and the softmax scales
-//       it by 4^-a.  High 2 bits of boosted channels are 16-32 extra
-//       reduction rows with A = 4 * q'[channel(rank)].
+//       Every MFMA of slot a accumulates 4^a sum_k A[k] c plus
+//       1024 sum_k A[k]; each tile starts from -1024 sum_k A[k] (bias tile
+//       X), the softmax scales it by 4^-a and subtracts Y = sum_k A[k] z_k
+//       (bias tile Y; 9 bias MFMAs in all).  High 2 bits of boosted channels
+//       are 16-32 extra reduction rows with A = 4 * q'[channel(rank)].
 //  softmax  online, base 2, one DPP row reduction per page.
 //  PV   O[h][d] = sum_t P'[h][t] * B[t][d], P' = p * s_t (fp16) staged
 //       through a 1-2 KB LDS buffer; value codes get the same tr8 + mask
@@ -112,12 +112,21 @@ __device__ __forceinline__ float dpp(float v)
 }
 
 // Reductions over the 16 lanes of a DPP row (one lane group = one head).
+// Max over the 16 lanes of a DPP row: one v_max_f32 with a row rotation per
+// step (fmaxf would add a DPP move and an input canonicalisation per step).
+// The s_nop 1 ahead of each step covers the two wait states a DPP read needs
+// after a VALU write of the same VGPR.  Scores are never NaN.
 __device__ __forceinline__ float row_max16(float v)
 {
-    v = fmaxf(v, dpp<0x128>(v));
-    v = fmaxf(v, dpp<0x124>(v));
-    v = fmaxf(v, dpp<0x122>(v));
-    v = fmaxf(v, dpp<0x121>(v));
+    asm volatile("s_nop 1\n\t"
+                 "v_max_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+                 "s_nop 1\n\t"
+                 "v_max_f32_dpp %0, %0, %0 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
+                 "s_nop 1\n\t"
+                 "v_max_f32_dpp %0, %0, %0 row_ror:2 row_mask:0xf bank_mask:0xf\n\t"
+                 "s_nop 1\n\t"
+                 "v_max_f32_dpp %0, %0, %0 row_ror:1 row_mask:0xf bank_mask:0xf"
+                 : "+v"(v));
     return v;
 }
 
@@ -305,6 +314,7 @@ struct WaveState {
     int prow;                                // head row whose P' this lane reads for PV
     float m_run[HPL], l_run[HPL];
     f32x4 O[2][4];
+    CodeMasks cm;                            // set once per wave: kept in VGPRs, not rebuilt per page
 };
 
 // One (page, head) record in LDS stage `st` -> QK, online softmax, PV.
@@ -316,7 +326,7 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     const int q = lane >> 4, r = lane & 15;
     const half8 neg1024 = __builtin_bit_cast(half8, u32x4{0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u});
 
-    const CodeMasks cm = code_masks();
+    const CodeMasks &cm = W.cm;
 
     // ---------------- operands from LDS, issued together
     u32x4 ks[4], kz[4];
@@ -341,20 +351,18 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     }
 
     // ---------------- QK A operands and the bias tiles X = -1024 sum A,
-    // Y = -sum A z (per head row, broadcast over token columns)
+    // Y = sum A z (per head row, broadcast over token columns)
     half8 A[4], Ahi;
     f32x4 Xt = {0.0f, 0.0f, 0.0f, 0.0f}, Yt = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        u32x4 av, nz;
+        u32x4 av;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 4; ++j)
             av[j] = as_u(as_h2(W.qv[s][j]) * as_h2(ks[s][j]));
-            nz[j] = kz[s][j] ^ 0x80008000u;
-        }
         A[s] = __builtin_bit_cast(half8, av);
         Xt = mfma(A[s], neg1024, Xt);
-        Yt = mfma(A[s], __builtin_bit_cast(half8, nz), Yt);
+        Yt = mfma(A[s], __builtin_bit_cast(half8, kz[s]), Yt);
     }
     if (Dk > 0) {
         u32x4 av;
@@ -373,15 +381,13 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     // is then most often in its VALU / memory phase, and the matrix core
     // stays fed (measured: 1.5-2 us less per launch at config 3).
     __builtin_amdgcn_s_setprio(1);
-    // ---------------- QK token tiles: S[cb][a] covers tokens 64cb + 4r + a
-    // and holds 4^a (S - bias) after the MFMAs below.
+    // ---------------- QK token tiles: S[cb][a] covers tokens 64cb + 4r + a.
+    // Every chain starts from X, so S[cb][a] ends at 4^a sum_k A c; the
+    // softmax subtracts the zero-point term Y.
     f32x4 S[2][4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-        const f32x4 init = Xt + Yt * (float)(1 << (2 * a));
-        S[0][a] = init;
-        S[1][a] = init;
-    }
+    for (int a = 0; a < 4; ++a)
+        S[0][a] = S[1][a] = Xt;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -434,19 +440,22 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
 #pragma unroll
             for (int a = 0; a < 4; ++a)
                 mx = fmaxf(mx, sv[cb][a]);
-        mx = row_max16(mx);
+        // scores are sv - Y: the max over the row and the exponents absorb Y
+        const float yk = Yt[ri];
+        mx = row_max16(mx) - yk;
         const float mn = fmaxf(W.m_run[j], mx);
         alpha[j] = __builtin_amdgcn_exp2f(W.m_run[j] - mn);
         W.m_run[j] = mn;
+        const float mny = mn + yk;
         float lsum = 0.0f, xsum = 0.0f, ysum = 0.0f;
         const int h = q * HPL + j;
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
             const u32x4 vm = cb ? vm1 : vm0;
-            const float p0v = __builtin_amdgcn_exp2f(sv[cb][0] - mn);
-            const float p1v = __builtin_amdgcn_exp2f(sv[cb][1] - mn);
-            const float p2v = __builtin_amdgcn_exp2f(sv[cb][2] - mn);
-            const float p3v = __builtin_amdgcn_exp2f(sv[cb][3] - mn);
+            const float p0v = __builtin_amdgcn_exp2f(sv[cb][0] - mny);
+            const float p1v = __builtin_amdgcn_exp2f(sv[cb][1] - mny);
+            const float p2v = __builtin_amdgcn_exp2f(sv[cb][2] - mny);
+            const float p3v = __builtin_amdgcn_exp2f(sv[cb][3] - mny);
             lsum += (p0v + p1v) + (p2v + p3v);
             // (scale, zero) pairs of tokens 64cb + 4r + {0..3}
             const half2v sv01 = as_h2(__builtin_amdgcn_perm(vm[1], vm[0], 0x05040100u));
@@ -559,6 +568,7 @@ void decode_mfma_kernel(DecodeParams p)
     __syncthreads();
 
     WaveState<GQ> W;
+    W.cm = code_masks();
     // Static halves of the QK A operand: q * sm_scale * log2(e) / 2^e for the
     // lane's 8 channels of every K-step; zero on rows that carry no head.
     const bool head_row = (r % ROWS_PER_HEAD) == 0;
