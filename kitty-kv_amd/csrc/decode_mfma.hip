@@ -19,7 +19,11 @@
 //       (bias tile Y; 9 bias MFMAs in all).  High 2 bits of boosted channels
 //       are 16-32 extra reduction rows with A = 4 * q'[channel(rank)].
 //  softmax  online, base 2, one DPP row reduction per page.
-//  PV   O[h][d] = sum_t P'[h][t] * B[t][d], P' = p * s_t (fp16) staged
+//  PV, GQA 4: v_mfma_f32_16x16x128_f8f6f4 with the value codes as fp4 B
+//       operands (ds_read_b64_tr_b4 + one mask per 8 codes) and P' as three
+//       fp8 terms on the three spare rows of each head (see pv_fp8_fp4):
+//       8 MFMAs per page instead of 32.
+//  PV, GQA 8 / 16: O[h][d] = sum_t P'[h][t] * B[t][d], P' = p * s_t (fp16) staged
 //       through a 1-2 KB LDS buffer; value codes get the same tr8 + mask
 //       treatment, so output tile a (channel slot a) accumulates 4^a O plus
 //       1024 sum_t P'; the per-token zero points and the 1024 offsets are
@@ -39,6 +43,9 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 // LDS stage of one (page, head) record, byte offsets.
 constexpr int kKlo = 0;       // key low bits   (128 rows x 32 B), chunk-swizzled
@@ -98,6 +105,44 @@ __device__ __forceinline__ half8 codes_to_half8(const RawCodes &r, const CodeMas
     v[2] = (r.w[1] & m.slot[A]) | m.one;
     v[3] = (r.w[3] & m.slot[A]) | m.one;
     return __builtin_bit_cast(half8, v);
+}
+
+// PV operands of the GQA-4 path (v_mfma_f32_16x16x128_f8f6f4, A fp8 e4m3,
+// B fp4 e2m1).  A 2-bit value code in the low bits of a nibble whose top
+// two bits are clear is the e2m1 number code / 2, so value codes become B
+// operands with one mask per 8 codes.  K order of the instruction: fp4 B
+// nibble i of lane group g is K = 32 g + i; fp8 A byte i of lane group g is
+// K = 16 g + i for i < 16 and 64 + 16 g + (i - 16) above.
+__device__ __forceinline__ i32x2 tr4(const unsigned char *lds)
+{
+    return __builtin_amdgcn_ds_read_tr4_b64_v2i32((__attribute__((address_space(3))) i32x2 *)lds);
+}
+
+__device__ __forceinline__ f32x4 mfma_fp8_fp4(i32x8 a, u32x4 b)
+{
+    const i32x8 b8 = {(int)b[0], (int)b[1], (int)b[2], (int)b[3], 0, 0, 0, 0};  // fp4 reads the first 4 registers
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b8, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 4, 0, 0, 0, 0);
+}
+
+// Four fp32 values / scale -> four fp8 e4m3 (round to nearest even) in one
+// dword, byte i = value i.  The caller keeps |value / scale| <= 448.
+__device__ __forceinline__ unsigned fp8x4(float a, float b, float c, float d, float scale)
+{
+    s16x2 v = __builtin_bit_cast(s16x2, a);  // both halves are overwritten
+    v = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(v, a, b, scale, false);
+    v = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(v, c, d, scale, true);
+    return __builtin_bit_cast(unsigned, v);
+}
+
+// x[i] -= (fp8 byte i of w) * scale: the residual the next fp8 term encodes.
+__device__ __forceinline__ void fp8_residual(float *x, unsigned w, float scale)
+{
+    const f32x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, scale, false);
+    const f32x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, scale, true);
+    x[0] -= lo[0];
+    x[1] -= lo[1];
+    x[2] -= hi[0];
+    x[3] -= hi[1];
 }
 
 __device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c)
@@ -313,9 +358,126 @@ struct WaveState {
     int tr_base0, tr_base1;                  // tr8 source offsets (byte columns 0-15 / 16-31)
     int prow;                                // head row whose P' this lane reads for PV
     float m_run[HPL], l_run[HPL];
-    f32x4 O[2][4];
+    f32x4 O[2][4];                           // GQA 8 / 16: output tiles (4^a O of channels 64cb + 4r + a)
+    float o4[4][2];                          // GQA 4: O of head q, channels 32ch + 2r + e
+    int trv[2][2];                           // GQA 4: tr4 offsets of value rows 32q + 16k + r, 16-byte chunk c
     CodeMasks cm;                            // set once per wave: kept in VGPRs, not rebuilt per page
 };
+
+// GQA 4: online softmax and PV of one page with fp8 x fp4 MFMAs.  Lane
+// (q, r) holds head q's scores of tokens 64cb + 4r + a (S[cb][a] register 0,
+// scaled by 4^a, zero-point term Y not yet subtracted).
+//  P' = p * s_t (value scale of token t) is written to LDS as three fp8
+//  terms on MFMA rows 4h + t: term 0 = fp8(P' / sig), term t encodes the
+//  remaining residual with scale sig / 16^t (about 12 significant bits in
+//  all).  sig = 2^(e - 8) with s_max < 2^e, the page's largest value scale,
+//  so P' / sig < 256 <= 448 (p <= 1).
+//  Value codes: two tr4 reads per 8-byte chunk ch give each lane the nibble
+//  of channels 32ch + 2r, +1 for tokens 32q + 0..31; the nibble masked with
+//  0x3 (even channel) or shifted down by 2 (odd) is the fp4 operand.
+//  O[h][d] += 2 sig (C0 + C1 / 16 + C2 / 256) - sum_t P'_t z_t, C_t = row
+//  4h + t of the MFMA output (fp4 value = code / 2).
+template <int GQ>
+__device__ __forceinline__ void pv_fp8_fp4(WaveState<GQ> &W, unsigned char *st, const f32x4 (&S)[2][4],
+                                           const f32x4 &Yt, int lane)
+{
+    const int q = lane >> 4, r = lane & 15;
+    i32x2 vr[4][2];  // [chunk][read]: tokens 32q + 16k + 0..15
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch)
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+            vr[ch][k] = tr4(st + kVal + W.trv[k][ch >> 1] + 8 * (ch & 1));
+
+    const u32x4 vm0 = *(const u32x4 *)(st + kMeta + 512 + 4 * (4 * r));
+    const u32x4 vm1 = *(const u32x4 *)(st + kMeta + 512 + 4 * (64 + 4 * r));
+    float sv[2][4];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+            sv[cb][a] = S[cb][a][0] * (1.0f / (float)(1 << (2 * a)));
+    float mx = sv[0][0];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+            mx = fmaxf(mx, sv[cb][a]);
+    const float yk = Yt[0];
+    mx = row_max16(mx) - yk;
+    const float mn = fmaxf(W.m_run[0], mx);
+    const float alpha = __builtin_amdgcn_exp2f(W.m_run[0] - mn);
+    W.m_run[0] = mn;
+    const float mny = mn + yk;
+
+    float x[2][4], lsum = 0.0f, ysum = 0.0f, smax = 0.0f;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        const u32x4 vm = cb ? vm1 : vm0;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            const half2v sz = as_h2(vm[a]);  // (scale, zero) of token 64cb + 4r + a
+            const float sc = (float)sz[0], zp = (float)sz[1];
+            const float pr = __builtin_amdgcn_exp2f(sv[cb][a] - mny);
+            lsum += pr;
+            x[cb][a] = pr * sc;
+            ysum = __builtin_fmaf(x[cb][a], zp, ysum);
+            smax = fmaxf(smax, sc);
+        }
+    }
+    W.l_run[0] = W.l_run[0] * alpha + lsum;
+    const float yv = row_sum16(ysum);
+    smax = row_max16(smax);
+    const float sig = __builtin_amdgcn_ldexpf(1.0f, __builtin_amdgcn_frexp_expf(smax) - 8);
+
+    unsigned char *pb = st + kKlo;  // 16 rows x 128 fp8, over the consumed key codes
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        float *xc = x[cb];
+        unsigned w0 = fp8x4(xc[0], xc[1], xc[2], xc[3], sig);
+        fp8_residual(xc, w0, sig);
+        unsigned w1 = fp8x4(xc[0], xc[1], xc[2], xc[3], sig * 0.0625f);
+        fp8_residual(xc, w1, sig * 0.0625f);
+        unsigned w2 = fp8x4(xc[0], xc[1], xc[2], xc[3], sig * 0.00390625f);
+        unsigned char *row = pb + 128 * (4 * q) + 64 * cb + 4 * r;
+        *(unsigned *)(row) = w0;
+        *(unsigned *)(row + 128) = w1;
+        *(unsigned *)(row + 256) = w2;
+    }
+
+    // A operand: row r of the P' terms (row 4h + 3 is never written; its
+    // output row is ignored).  Inline asm for the reason given in
+    // compute_page (no wait for the other stage's prefetch).
+    __builtin_amdgcn_s_setprio(1);
+    i32x8 Ap;
+    {
+        u32x4 a0, a1;
+        const unsigned addr = (unsigned)(uintptr_t)(pb + 128 * r + 16 * q);
+        asm volatile("ds_read_b128 %0, %2\n\t"
+                     "ds_read_b128 %1, %2 offset:64\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=v"(a0), "=v"(a1)
+                     : "v"(addr)
+                     : "memory");
+        Ap = i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+    }
+    const float s2 = 2.0f * sig;
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) {
+        const unsigned m = 0x33333333u;
+        const u32x4 ev = {(unsigned)vr[ch][0][0] & m, (unsigned)vr[ch][0][1] & m, (unsigned)vr[ch][1][0] & m,
+                          (unsigned)vr[ch][1][1] & m};
+        const u32x4 od = {((unsigned)vr[ch][0][0] >> 2) & m, ((unsigned)vr[ch][0][1] >> 2) & m,
+                          ((unsigned)vr[ch][1][0] >> 2) & m, ((unsigned)vr[ch][1][1] >> 2) & m};
+        const f32x4 ce = mfma_fp8_fp4(Ap, ev);
+        const f32x4 co = mfma_fp8_fp4(Ap, od);
+        const float ve = __builtin_fmaf(ce[2], 0.00390625f, __builtin_fmaf(ce[1], 0.0625f, ce[0]));
+        const float vo = __builtin_fmaf(co[2], 0.00390625f, __builtin_fmaf(co[1], 0.0625f, co[0]));
+        W.o4[ch][0] = __builtin_fmaf(W.o4[ch][0], alpha, __builtin_fmaf(ve, s2, -yv));
+        W.o4[ch][1] = __builtin_fmaf(W.o4[ch][1], alpha, __builtin_fmaf(vo, s2, -yv));
+    }
+    __builtin_amdgcn_s_setprio(0);
+}
 
 // One (page, head) record in LDS stage `st` -> QK, online softmax, PV.
 template <int GQ>
@@ -410,6 +572,10 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     }
 
     __builtin_amdgcn_s_setprio(0);
+    if constexpr (GQ == 4) {
+        pv_fp8_fp4(W, st, S, Yt, lane);
+        return;
+    }
     // value codes for PV, issued before the softmax so they arrive meanwhile
     i32x2 vraw[4][2];
 #pragma unroll
@@ -613,6 +779,15 @@ void decode_mfma_kernel(DecodeParams p)
         W.tr_base0 = 32 * tr_row + 16 * (0 ^ (q & 1)) + 8 * (r & 1);
         W.tr_base1 = 32 * tr_row + 16 * (1 ^ (q & 1)) + 8 * (r & 1);
     }
+    // tr4 offsets of value rows R = 32q + 16k + r (GQA 4): 16-byte chunk c of
+    // row R sits at 32 R + 16 (c ^ ((R >> 3) & 1)) in the stage.
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int R = 32 * q + 16 * k + r;
+            W.trv[k][c] = 32 * R + 16 * (c ^ ((R >> 3) & 1));
+        }
 #pragma unroll
     for (int j = 0; j < HPL; ++j) {
         W.m_run[j] = -__builtin_inff();
@@ -623,6 +798,9 @@ void decode_mfma_kernel(DecodeParams p)
 #pragma unroll
         for (int a = 0; a < 4; ++a)
             W.O[cb][a] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch)
+        W.o4[ch][0] = W.o4[ch][1] = 0.0f;
     __syncthreads();  // rank_chan reads done before stage1 is overwritten
 
     // Page ids of this split (at most 64, see choose_pages_per_split), one
@@ -689,14 +867,25 @@ void decode_mfma_kernel(DecodeParams p)
         const int h = q * HPL + j;
         const int64_t row = ((int64_t)b * p.Hq + kh * GQ + h) * NS + split;
         float *o = p.ws_o + row * 128;
+        if constexpr (GQ == 4) {
+            // o4[ch][e] is O of channel 32ch + 2r + e
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            // output tile a holds 4^a O for channels 64cb + 4r + a
-            float4 v = make_float4(W.O[cb][0][j * RSTEP], W.O[cb][1][j * RSTEP] * 0.25f,
-                                   W.O[cb][2][j * RSTEP] * 0.0625f, W.O[cb][3][j * RSTEP] * 0.015625f);
-            if (poison)
-                v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
-            *(float4 *)(o + 64 * cb + 4 * r) = v;
+            for (int ch = 0; ch < 4; ++ch) {
+                float2 v = make_float2(W.o4[ch][0], W.o4[ch][1]);
+                if (poison)
+                    v = make_float2(__builtin_nanf(""), __builtin_nanf(""));
+                *(float2 *)(o + 32 * ch + 2 * r) = v;
+            }
+        } else {
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                // output tile a holds 4^a O for channels 64cb + 4r + a
+                float4 v = make_float4(W.O[cb][0][j * RSTEP], W.O[cb][1][j * RSTEP] * 0.25f,
+                                       W.O[cb][2][j * RSTEP] * 0.0625f, W.O[cb][3][j * RSTEP] * 0.015625f);
+                if (poison)
+                    v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+                *(float4 *)(o + 64 * cb + 4 * r) = v;
+            }
         }
         if (r == 0) {
             p.ws_ml[2 * row] = poison ? __builtin_nanf("") : W.m_run[j];
