@@ -141,8 +141,9 @@ int kitty_dequantize_value_page(const kitty_page_store *store, int64_t page, int
  * Pools must be the contiguous tensors of PageCentricKVLayoutManager (16-byte
  * aligned bases); page ids are int32 and byte offsets are 64-bit, so a pool
  * may fill the whole 288 GB of an MI355X.
- * The workspace (device memory, size from kitty_decode_workspace_size) holds
- * the split-K partial results; it is scratch the caller owns.
+ * The workspace (device memory, size from kitty_decode_workspace_size,
+ * 16-byte aligned) holds the split-K partial results; it is scratch the
+ * caller owns.
  */
 typedef struct {
     const uint16_t *ptr;

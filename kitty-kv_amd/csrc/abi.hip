@@ -135,6 +135,8 @@ static int prepare(const kitty_decode_args *args, DecodeParams &p)
     const size_t need = workspace_bytes(p);
     if (!args->workspace || args->workspace_bytes < need)
         return fail(KITTY_E_INVALID, "workspace too small: need " + std::to_string(need) + " bytes");
+    if ((uintptr_t)args->workspace & 15)
+        return fail(KITTY_E_INVALID, "workspace must be 16-byte aligned");
     p.ws_o = (float *)args->workspace;
     p.ws_ml = p.ws_o + (size_t)p.B * p.Hq * (p.n_splits + 1) * p.D;
     return KITTY_OK;

@@ -264,10 +264,26 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
 }
 
 // Combine the n_splits + 1 partials of (b, qh) and write the fp16 output.
-// One wave per (b, qh); each lane owns channels lane and lane + 64 (D <= 128
-// per pass).  Splits are taken 32 at a time with every load of a batch
-// issued together, and merged with a running maximum, so a batch costs one
-// memory round trip (config 3 has 17 partials per row: one batch).
+// One wave per (b, qh).  Pass 1: the running maximum M over all splits (one
+// split per lane per step) and the NaN flag.  Pass 2, per 128 channels: lane
+// l owns channels 2l, 2l + 1; splits are taken 32 at a time, every load of a
+// batch issued together (one float2 of O per split and lane, one (m, l) pair
+// per lane; indices past the last split are clamped and weigh 0), so config
+// 3 (17 partials per row) costs one memory round trip after pass 1.
+__device__ __forceinline__ float wave_max(float v)
+{
+    for (int off = 32; off > 0; off >>= 1)
+        v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+    for (int off = 32; off > 0; off >>= 1)
+        v += __shfl_xor(v, off);
+    return v;
+}
+
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
 {
     constexpr int kBatch = 32;
@@ -277,50 +293,54 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
     const int NS = p.n_splits + 1;
     const int64_t row0 = (int64_t)bq * NS;
     const float ninf = -__builtin_inff();
+
+    float M = ninf;
+    int nan = 0;
+    for (int s = lane; s < NS; s += 64) {
+        const float m = p.ws_ml[2 * (row0 + s)];
+        nan |= m != m;
+        M = fmaxf(M, m);
+    }
+    M = wave_max(M);
+    nan = wave_max((float)nan) > 0.0f;
+
+    uint16_t *o = p.out + b * p.out_s_seq + qh * p.out_s_head;
+    float L = 0.0f;
     for (int d0 = 0; d0 < p.D; d0 += 128) {
-        const int da = d0 + lane, db = d0 + 64 + lane;
-        float M = ninf, L = 0.0f, acc_a = 0.0f, acc_b = 0.0f;
-        bool nan = false;
+        const int d = d0 + 2 * lane;            // D is a multiple of 4: d < D implies d + 1 < D
+        const int dd = d < p.D ? d : p.D - 2;   // clamped: every lane loads
+        float ax = 0.0f, ay = 0.0f, lsum = 0.0f;
         for (int s0 = 0; s0 < NS; s0 += kBatch) {
-            float m[kBatch], l[kBatch], oa[kBatch], ob[kBatch];
+            const int sl = min(s0 + lane, NS - 1);
+            const float2 ml = *(const float2 *)(p.ws_ml + 2 * (row0 + sl));
+            float2 v[kBatch];
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
-                const bool ok = s0 + u < NS;
-                const int64_t row = row0 + (ok ? s0 + u : 0);
-                const float2 ml = ok ? *(const float2 *)(p.ws_ml + 2 * row) : make_float2(ninf, 0.0f);
-                m[u] = ml.x;
-                l[u] = ml.y;
-                oa[u] = ok && da < p.D ? p.ws_o[row * p.D + da] : 0.0f;
-                ob[u] = ok && db < p.D ? p.ws_o[row * p.D + db] : 0.0f;
+                const int64_t row = row0 + min(s0 + u, NS - 1);
+                v[u] = *(const float2 *)(p.ws_o + row * p.D + dd);
             }
-            float bm = ninf;
+            const bool live = lane < kBatch && s0 + lane < NS && ml.x != ninf && M != ninf;
+            const float w = live ? exp2f(ml.x - M) : 0.0f;
+            lsum += w * ml.y;
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
-                nan |= m[u] != m[u];
-                bm = fmaxf(bm, m[u]);
+                const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
+                ax += wu * v[u].x;
+                ay += wu * v[u].y;
             }
-            const float Mn = fmaxf(M, bm);
-            if (Mn == ninf)
-                continue;  // nothing attended yet
-            const float r = exp2f(M - Mn);
-            L *= r;
-            acc_a *= r;
-            acc_b *= r;
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const float w = m[u] != ninf ? exp2f(m[u] - Mn) : 0.0f;
-                L += l[u] * w;
-                acc_a += oa[u] * w;
-                acc_b += ob[u] * w;
-            }
-            M = Mn;
         }
+        if (d0 == 0)
+            L = wave_sum(lsum);
         const float inv = L > 0.0f ? 1.0f / L : 0.0f;  // no tokens -> zeros (attention.py:180-182)
-        uint16_t *o = p.out + b * p.out_s_seq + qh * p.out_s_head;
-        if (da < p.D)
-            o[da] = f2h(nan ? __builtin_nanf("") : acc_a * inv);
-        if (db < p.D)
-            o[db] = f2h(nan ? __builtin_nanf("") : acc_b * inv);
+        if (d < p.D) {
+            const float x = nan ? __builtin_nanf("") : ax * inv, y = nan ? __builtin_nanf("") : ay * inv;
+            if (((uintptr_t)o & 3) == 0) {
+                *(uint32_t *)(o + d) = (uint32_t)f2h(x) | ((uint32_t)f2h(y) << 16);
+            } else {
+                o[d] = f2h(x);
+                o[d + 1] = f2h(y);
+            }
+        }
     }
 }
 
