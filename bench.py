@@ -250,19 +250,21 @@ def main() -> int:
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / K
     step_us_events = e0.elapsed_time(e1) / K * 1e3
-    # kernel durations: an event pair around each launch of the split kernel
-    # (the dominant one) and of the merge kernel
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
-    for i in range(K):
-        p = plans[i % len(plans)]
-        ev[i][0].record()
-        p.run_splits()
-        ev[i][1].record()
-        p.run_merge()
-        ev[i][2].record()
-    torch.cuda.synchronize()
-    kernel_us = sum(e[0].elapsed_time(e[1]) for e in ev) / K * 1e3
-    merge_us = sum(e[1].elapsed_time(e[2]) for e in ev) / K * 1e3
+    # kernel durations: K back-to-back launches of the split kernel (the
+    # dominant one), then K of the merge kernel, each burst between two HIP
+    # events on the launch stream (an event pair per launch would add the
+    # dispatch latency of every launch to the kernel time)
+    def burst(fn) -> float:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for i in range(K):
+            fn(plans[i % len(plans)])
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / K * 1e3
+    kernel_us = burst(lambda p: p.run_splits())
+    merge_us = burst(lambda p: p.run_merge())
     log(f"{ms_per_step * 1e3:.1f} us/step wall ({step_us_events:.1f} by events); "
         f"split kernel {kernel_us:.1f} us, merge {merge_us:.1f} us")
     achieved = nb["total"] / (kernel_us * 1e-6) / 1e9
