@@ -32,6 +32,8 @@ HBM_PEAK_GBPS = 8000.0
 
 CONFIGS = {
     "cfg3": dict(B=16, Hq=32, Hkv=8, ctx=32768, boost=0.125, outlier=8.0, seed=3),
+    # config 4: ragged contexts drawn uniformly from [512, 65536] (seeded), 25 % INT4
+    "cfg4": dict(B=64, Hq=32, Hkv=8, ctx=(512, 65536), boost=0.25, outlier=8.0, seed=4),
     "cfg5": dict(B=4, Hq=64, Hkv=8, ctx=131072, boost=0.125, outlier=16.0, seed=5),
 }
 D, G, S = 128, 128, 32
@@ -43,11 +45,18 @@ def log(msg: str) -> None:
 
 def build_workload(torch, dev, cfg, copies: int, placement_kind: str = "shuffled"):
     from kitty.kernels.ops import DecodePlan, pool_store, quantize_into_pools
-    B, Hq, Hkv, ctx = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["ctx"]
+    import numpy as np
+    B, Hq, Hkv = cfg["B"], cfg["Hq"], cfg["Hkv"]
+    if isinstance(cfg["ctx"], tuple):   # ragged: per-sequence contexts from a seeded draw
+        ctxs = np.random.default_rng(cfg["seed"]).integers(cfg["ctx"][0], cfg["ctx"][1] + 1, size=B)
+    else:
+        ctxs = np.full(B, cfg["ctx"])
     dk = round(cfg["boost"] * D)
     sentinel = min(dk + 1, 255)
-    n_pages = (ctx - S) // G
-    n_tail = (ctx - S) % G
+    np_list = [(int(c) - S) // G for c in ctxs]
+    tail_list = [(int(c) - S) % G for c in ctxs]
+    n_pages, n_tail = max(np_list), max(tail_list)
+    pages_per_copy = sum(np_list)
     gen = torch.Generator(device="cpu").manual_seed(cfg["seed"])
     chans = torch.stack([torch.randperm(D, generator=gen)[:dk] for _ in range(Hkv)])
     calib = torch.randn(256, Hkv, D, generator=gen)
@@ -60,7 +69,7 @@ def build_workload(torch, dev, cfg, copies: int, placement_kind: str = "shuffled
         bi[torch.arange(Hkv), order[:, r]] = r
     bi = bi.to(dev)
 
-    used = copies * B * n_pages
+    used = copies * pages_per_copy
     P = used + 8
     kb = torch.empty(P, Hkv, D, G // 4, dtype=torch.uint8, device=dev)
     kh = torch.empty(P, Hkv, dk, G // 4, dtype=torch.uint8, device=dev)
@@ -70,8 +79,10 @@ def build_workload(torch, dev, cfg, copies: int, placement_kind: str = "shuffled
     store = pool_store(kb, kh, km, vp, vm)
     if placement_kind == "shuffled":      # a fragmented pool: pages from a shuffled free list
         placement = torch.randperm(P, generator=gen)[:used].to(torch.int32)
-    else:                                 # first-fit, B sequences growing in lockstep: page p of seq b
+    elif len(set(np_list)) == 1:          # first-fit, B sequences growing in lockstep: page p of seq b
         placement = torch.arange(used, dtype=torch.int32).view(copies, n_pages, B).transpose(1, 2).reshape(-1)
+    else:
+        placement = torch.arange(used, dtype=torch.int32)
     g = torch.Generator(device=dev).manual_seed(cfg["seed"] + 100)
     scale = torch.ones(Hkv, D, device=dev)
     for h in range(Hkv):
@@ -89,26 +100,33 @@ def build_workload(torch, dev, cfg, copies: int, placement_kind: str = "shuffled
     sv = torch.randn(B, Hkv, S, D, device=dev, generator=g).half()
     tk = torch.randn(B, Hkv, max(n_tail, 1), D, device=dev, generator=g).half()
     tv = torch.randn(B, Hkv, max(n_tail, 1), D, device=dev, generator=g).half()
-    npg = torch.full((B,), n_pages, dtype=torch.int32, device=dev)
+    npg = torch.tensor(np_list, dtype=torch.int32, device=dev)
     sl = torch.full((B,), S, dtype=torch.int32, device=dev)
-    tl = torch.full((B,), n_tail, dtype=torch.int32, device=dev)
+    tl = torch.tensor(tail_list, dtype=torch.int32, device=dev)
     out = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
     plans, tables = [], []
     for c in range(copies):
-        bt = placement[c * B * n_pages:(c + 1) * B * n_pages].view(B, n_pages).contiguous().to(dev)
+        bt = torch.zeros(B, n_pages, dtype=torch.int32)
+        off = c * pages_per_copy
+        for b in range(B):
+            bt[b, :np_list[b]] = placement[off:off + np_list[b]]
+            off += np_list[b]
+        bt = bt.to(dev)
         tables.append(bt)
         plans.append(DecodePlan(q, bt, npg, kb, kh, km, vp, vm, bi, sk, sv, sl, tk, tv, tl, out=out))
-    w = dict(B=B, Hq=Hq, Hkv=Hkv, dk=dk, n_pages=n_pages, n_tail=n_tail, P=P, pools=(kb, kh, km, vp, vm),
-             tables=tables, q=q, sk=sk, sv=sv, tk=tk, tv=tv, bi=bi, plans=plans, out=out)
+    w = dict(B=B, Hq=Hq, Hkv=Hkv, dk=dk, n_pages=n_pages, n_tail=n_tail, np_list=np_list, tail_list=tail_list,
+             P=P, pools=(kb, kh, km, vp, vm), tables=tables, q=q, sk=sk, sv=sv, tk=tk, tv=tv, bi=bi, plans=plans,
+             out=out)
     return w
 
 
 def algorithmic_bytes(w) -> dict:
-    B, Hkv, Hq, n_pages, dk = w["B"], w["Hkv"], w["Hq"], w["n_pages"], w["dk"]
+    B, Hkv, Hq, dk = w["B"], w["Hkv"], w["Hq"], w["dk"]
+    pages = sum(w["np_list"])
     per_page_head = D * G // 4 + dk * G // 4 + 2 * D * 2 + G * D // 4 + G * 2 * 2
-    packed = B * Hkv * n_pages * per_page_head
-    fp16 = B * Hkv * (S + w["n_tail"]) * D * 2 * 2
-    small = B * Hq * D * 2 + B * n_pages * 4 + Hkv * D + 3 * B * 4   # q, block table, boost_idx, lengths
+    packed = Hkv * pages * per_page_head
+    fp16 = Hkv * sum(S + t for t in w["tail_list"]) * D * 2 * 2
+    small = B * Hq * D * 2 + pages * 4 + Hkv * D + 3 * B * 4   # q, block table, boost_idx, lengths
     return dict(per_page_head=per_page_head, packed=packed, fp16=fp16, total=packed + fp16 + small)
 
 
@@ -121,24 +139,27 @@ def cpu_baseline(w, budget_s: float) -> dict:
     O.build()
     kb, kh, km, vp, vm = w["pools"]
     bt = w["tables"][0]
-    n = w["n_tail"]
-    done, t_total = 0, 0.0
+    done, t_total, pages_done = 0, 0.0, 0
     while done < w["B"] and (t_total < budget_s or done == 0):
         b = done
-        idx = bt[b].long()
+        npb, n = w["np_list"][b], w["tail_list"][b]
+        idx = bt[b, :npb].long()
         sub = [t[idx].cpu().numpy() for t in (kb, kh, km, vp, vm)]
-        args = (w["q"][b].cpu().numpy(), np.arange(w["n_pages"], dtype=np.int32), *sub, w["bi"].cpu().numpy(),
+        args = (w["q"][b].cpu().numpy(), np.arange(npb, dtype=np.int32), *sub, w["bi"].cpu().numpy(),
                 w["dk"], w["sk"][b].cpu().numpy(), w["sv"][b].cpu().numpy(), w["tk"][b, :, :n].cpu().numpy(),
                 w["tv"][b, :, :n].cpu().numpy(), w["Hq"], w["Hkv"], D)
         t0 = time.perf_counter()
         O.paged_attention(*args, n_threads=1)
         t_total += time.perf_counter() - t0
         done += 1
-    per_seq = t_total / done
-    return {"value": round(per_seq * w["B"] * 1e6, 1), "unit": "us/layer-step", "cores": 1, "kind": "port",
-            "sample": f"{done} of {w['B']} sequences (all {w['Hkv']} KV heads, {w['n_pages']} pages + "
-                      f"{S} sinks + {n} tail tokens each) through oracle/kitty_oracle.c "
-                      f"(paged_attention_reference restated), single thread; x{w['B']}/{done} to one layer-step"}
+        pages_done += npb
+    # scale by pages: the oracle's time is linear in the pages it walks
+    total_pages = sum(w["np_list"])
+    value = t_total * total_pages / max(pages_done, 1)
+    return {"value": round(value * 1e6, 1), "unit": "us/layer-step", "cores": 1, "kind": "port",
+            "sample": f"{done} of {w['B']} sequences ({pages_done} of {total_pages} pages, all {w['Hkv']} KV heads, "
+                      f"{S} sinks + FP16 tail each) through oracle/kitty_oracle.c (paged_attention_reference "
+                      f"restated), single thread; scaled by pages to one layer-step"}
 
 
 def bench_quantize(torch, dev, reps: int = 64) -> dict:
@@ -294,11 +315,12 @@ def main() -> int:
             cfg["outlier"]),
         "config": {"workload": f"{args.config}: B{cfg['B']} Hq{cfg['Hq']} Hkv{cfg['Hkv']} d{D} ctx{cfg['ctx']} "
                                f"S{S} G{G} {int(cfg['boost'] * 100 * 10) / 10}% INT4 keys, INT2 values",
-                   "batch": cfg["B"], "context": cfg["ctx"], "pages_per_seq": w["n_pages"],
+                   "batch": cfg["B"], "context": cfg["ctx"] if not isinstance(cfg["ctx"], tuple) else list(cfg["ctx"]),
+                   "pages_per_seq": w["n_pages"] if len(set(w["np_list"])) == 1 else sum(w["np_list"]) / cfg["B"],
                    "tail_tokens": w["n_tail"], "pool_copies": len(plans), "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "decode_mfma_kernel<4> (split-K phase of kitty_paged_decode)",
+                     "kernel": f"decode_mfma_kernel<{cfg['Hq'] // cfg['Hkv']}> (split-K phase of kitty_paged_decode)",
                      "kernel_us": round(kernel_us, 2), "merge_us": round(merge_us, 2),
                      "step_us_events": round(step_us_events, 2),
                      "algorithmic_bytes": nb["total"], "packed_kv_bytes": nb["packed"],
