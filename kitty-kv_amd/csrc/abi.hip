@@ -28,13 +28,13 @@ static int64_t resident_waves()
 // round of waves, because a handful of waves left over for a second round
 // doubles the kernel time.  Splits hold 4..kMaxPagesPerSplit pages (one page
 // id per lane of a wave).
-static int choose_pages_per_split(const kitty_decode_args &a)
+static int choose_pages_per_split(const kitty_decode_args &a, int n_fp16)
 {
     if (a.pages_per_split > 0)
         return a.pages_per_split > kMaxPagesPerSplit ? kMaxPagesPerSplit : a.pages_per_split;
     const int64_t pairs = (int64_t)a.batch * a.num_kv_heads;
     const int64_t per_pair = resident_waves() / (pairs > 0 ? pairs : 1);
-    const int64_t splits = per_pair >= 2 ? per_pair - 1 : 1;
+    const int64_t splits = per_pair > n_fp16 ? per_pair - n_fp16 : 1;
     int64_t pps = (a.max_pages + splits - 1) / splits;
     if (pps < 4)
         pps = 4;
@@ -93,7 +93,12 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
     p.Dk = a.d_boost;
     p.max_pages = a.max_pages;
     p.flags = a.flags;
-    p.pages_per_split = choose_pages_per_split(a);
+    // FP16 sinks + tail: one split per GQA group of 4 query heads in the MFMA
+    // kernel (its VALU FP16 path costs grow with the group), one otherwise.
+    p.n_fp16 = 1;
+    if (mfma_path_supported(p) && p.GQ > 4)
+        p.n_fp16 = p.GQ / 4;
+    p.pages_per_split = choose_pages_per_split(a, p.n_fp16);
     p.n_splits = (a.max_pages + p.pages_per_split - 1) / p.pages_per_split;
     p.sm_scale = a.sm_scale;
     return KITTY_OK;
@@ -101,7 +106,7 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
 
 static size_t workspace_bytes(const DecodeParams &p)
 {
-    const size_t rows = (size_t)p.B * p.Hq * (p.n_splits + 1);
+    const size_t rows = (size_t)p.B * p.Hq * num_partials(p);
     return rows * p.D * sizeof(float) + rows * 2 * sizeof(float);
 }
 
@@ -138,7 +143,7 @@ static int prepare(const kitty_decode_args *args, DecodeParams &p)
     if ((uintptr_t)args->workspace & 15)
         return fail(KITTY_E_INVALID, "workspace must be 16-byte aligned");
     p.ws_o = (float *)args->workspace;
-    p.ws_ml = p.ws_o + (size_t)p.B * p.Hq * (p.n_splits + 1) * p.D;
+    p.ws_ml = p.ws_o + (size_t)p.B * p.Hq * num_partials(p) * p.D;
     return KITTY_OK;
 }
 

@@ -28,11 +28,15 @@ struct DecodeParams {
     int sink_cap, tail_cap;
     int B, Hq, Hkv, GQ, D, G, Dk;
     int max_pages, pages_per_split, n_splits;
+    int n_fp16;   // FP16 splits per (b, kh): each takes an equal share of the sink + tail tokens
     int flags;
     float sm_scale;
     float *ws_o;  // [B][Hq][n_splits + 1][D] unnormalised partial outputs
     float *ws_ml; // [B][Hq][n_splits + 1][2] running max (log2 domain) and sum
 };
+
+// Partials per (b, query head): page splits, then FP16 splits.
+__host__ __device__ inline int num_partials(const DecodeParams &p) { return p.n_splits + p.n_fp16; }
 
 size_t generic_lds_bytes(int GQ, int D, int G, int Dk);
 int launch_generic(const DecodeParams &p, hipStream_t stream);

@@ -1,11 +1,12 @@
 // Split-K paged decode attention over Kitty's dense-sparse pages (gfx950).
 //
 // Work decomposition (flash-decoding): for every (sequence b, KV head kh) the
-// quantised pages are cut into splits of `pages_per_split` pages; one extra
-// split per (b, kh) attends the FP16 sinks and tail.  Each split produces,
+// quantised pages are cut into splits of `pages_per_split` pages; `n_fp16`
+// extra splits per (b, kh) attend the FP16 sinks and tail, each an equal
+// share of their tokens.  Each split produces,
 // for every query head of the GQA group, an unnormalised partial
 // (O, m, l) in base-2 online-softmax form; a merge kernel combines the
-// n_splits + 1 partials of (b, qh) into the fp16 output.  The result equals
+// num_partials partials of (b, qh) into the fp16 output.  The result equals
 // softmax(q K^T / sqrt(D)) V over sinks ‖ dequantised pages ‖ tail, which is
 // paged_attention_reference (kitty/kernels/attention.py:136-189).
 //
@@ -250,7 +251,7 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
         }
     }
     // ---------------------------------------------------- write partial
-    const int NS = p.n_splits + 1;
+    const int NS = num_partials(p);
     for (int e = tid; e < GQ * D; e += kGenThreads) {
         const int g = e / D, d = e - g * D;
         const int64_t row = ((int64_t)b * p.Hq + kh * GQ + g) * NS + split;
@@ -263,7 +264,7 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
     }
 }
 
-// Combine the n_splits + 1 partials of (b, qh) and write the fp16 output.
+// Combine the num_partials(p) partials of (b, qh) and write the fp16 output.
 // One wave per (b, qh).  Pass 1: the running maximum M over all splits (one
 // split per lane per step) and the NaN flag.  Pass 2, per 128 channels: lane
 // l owns channels 2l, 2l + 1; splits are taken 32 at a time, every load of a
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
     const int lane = threadIdx.x;
     const int bq = blockIdx.x;
     const int b = bq / p.Hq, qh = bq - b * p.Hq;
-    const int NS = p.n_splits + 1;
+    const int NS = num_partials(p);
     const int64_t row0 = (int64_t)bq * NS;
     const float ninf = -__builtin_inff();
 
@@ -357,7 +358,7 @@ int launch_generic(const DecodeParams &p, hipStream_t stream)
     const size_t lds = generic_lds_bytes(p.GQ, p.D, p.G, p.Dk);
     if (lds > 160 * 1024)
         return fail(KITTY_E_UNSUPPORTED, "generic decode needs more than 160 KB of LDS for this shape");
-    dim3 grid(p.n_splits + 1, p.Hkv, p.B);
+    dim3 grid(num_partials(p), p.Hkv, p.B);
     const void *fn = nullptr;
     switch (p.GQ) {
     case 1: fn = (const void *)decode_generic_kernel<1>; break;

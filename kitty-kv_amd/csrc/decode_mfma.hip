@@ -250,7 +250,7 @@ __device__ __forceinline__ void wait_vmcnt()
 // loads), then lane l accumulates channels 2l, 2l+1 over the chunk, reading
 // 16 value rows per batch of independent loads.
 template <int GQ>
-__device__ void fp16_segments(const DecodeParams &p, int b, int kh, float *qs, float *pb, float *m_out,
+__device__ void fp16_segments(const DecodeParams &p, int b, int kh, int part, float *qs, float *pb, float *m_out,
                               float *l_out, float (*O)[2])
 {
     const int lane = threadIdx.x;
@@ -266,14 +266,17 @@ __device__ void fp16_segments(const DecodeParams &p, int b, int kh, float *qs, f
     }
     __syncthreads();
     const int ns = min(max(0, p.sink_len[b]), p.sink_cap), nt = min(max(0, p.tail_len[b]), p.tail_cap);
+    // this split's share of the concatenated sink + tail tokens
+    const int lo = (int)((int64_t)(ns + nt) * part / p.n_fp16), hi = (int)((int64_t)(ns + nt) * (part + 1) / p.n_fp16);
     for (int seg = 0; seg < 2; ++seg) {
         const kitty_fp16_seg &K = seg == 0 ? p.sink_k : p.tail_k;
         const kitty_fp16_seg &V = seg == 0 ? p.sink_v : p.tail_v;
-        const int n = seg == 0 ? ns : nt;
+        const int base = seg == 0 ? 0 : ns;
+        const int s0 = max(lo - base, 0), s1 = min(hi - base, seg == 0 ? ns : nt);
         const uint16_t *kb = K.ptr + b * K.s_seq + kh * K.s_head;
         const uint16_t *vb = V.ptr + b * V.s_seq + kh * V.s_head;
-        for (int c0 = 0; c0 < n; c0 += 64) {
-            const int cnt = min(64, n - c0);
+        for (int c0 = s0; c0 < s1; c0 += 64) {
+            const int cnt = min(64, s1 - c0);
             const uint16_t *row = kb + (int64_t)(c0 + min(lane, cnt - 1)) * K.s_tok;
             float sc[GQ];
 #pragma unroll
@@ -698,11 +701,11 @@ void decode_mfma_kernel(DecodeParams p)
 
     const int lane = threadIdx.x, q = lane >> 4, r = lane & 15;
     const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
-    const int NS = p.n_splits + 1;
+    const int NS = num_partials(p);
 
-    if (split == p.n_splits) {
+    if (split >= p.n_splits) {
         float m[GQ], l[GQ], O[GQ][2];
-        fp16_segments<GQ>(p, b, kh, (float *)stage0, (float *)stage1, m, l, O);
+        fp16_segments<GQ>(p, b, kh, split - p.n_splits, (float *)stage0, (float *)stage1, m, l, O);
         for (int g = 0; g < GQ; ++g) {
             const int64_t row = ((int64_t)b * p.Hq + kh * GQ + g) * NS + split;
             *(float2 *)(p.ws_o + row * 128 + 2 * lane) = make_float2(O[g][0], O[g][1]);
@@ -910,7 +913,7 @@ bool mfma_path_supported(const DecodeParams &p)
 
 int launch_mfma(const DecodeParams &p, hipStream_t stream)
 {
-    dim3 grid(p.n_splits + 1, p.Hkv, p.B);
+    dim3 grid(num_partials(p), p.Hkv, p.B);
     switch (p.GQ) {
     case 4: hipLaunchKernelGGL(decode_mfma_kernel<4>, grid, dim3(64), 0, stream, p); break;
     case 8: hipLaunchKernelGGL(decode_mfma_kernel<8>, grid, dim3(64), 0, stream, p); break;
