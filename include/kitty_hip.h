@@ -143,7 +143,9 @@ int kitty_dequantize_value_page(const kitty_page_store *store, int64_t page, int
  * may fill the whole 288 GB of an MI355X.
  * The workspace (device memory, size from kitty_decode_workspace_size,
  * 16-byte aligned) holds the split-K partial results; it is scratch the
- * caller owns.
+ * caller owns.  The size depends on the shapes and the device, not on the
+ * page counts: the production shape splits the work by page counts read on
+ * the device (equal work per wave, ragged batches included).
  */
 typedef struct {
     const uint16_t *ptr;
@@ -183,7 +185,8 @@ typedef struct {
 
     int32_t batch, num_q_heads, num_kv_heads, head_dim, page_tokens, d_boost;
     int32_t max_pages;       /* >= every num_pages[b]; sizes the split grid */
-    int32_t pages_per_split; /* 0 = choose automatically */
+    int32_t pages_per_split; /* 0 = choose automatically; > 0: at least this many
+                                pages (production shape: work units) per split */
     int32_t flags;           /* KITTY_DECODE_* bits */
     float sm_scale;          /* 1/sqrt(D) in the reference (:172) */
 

@@ -1,5 +1,6 @@
 // C ABI entry points of libkitty_hip.so that are not kernel-specific:
 // version, error reporting, and the paged decode dispatcher.
+#include <algorithm>
 #include <string>
 
 #include "common.h"
@@ -12,16 +13,37 @@ static thread_local std::string g_last_error;
 void set_error(const std::string &msg) { g_last_error = msg; }
 const char *get_error() { return g_last_error.c_str(); }
 
-// Waves of the MFMA decode kernel resident on the current device at once:
-// 8 per CU (20 KB of LDS and 256 registers each), 2048 on an MI355X.
-static int64_t resident_waves()
+// Waves of the decode kernels resident on the current device at once:
+// waves_per_cu per CU (MFMA kernel: 8 for GQA groups of 4 and 8, with 20 KB
+// of LDS and 256 registers each, 4 for 16), 2048 / 1024 on an MI355X.
+static int64_t resident_waves(int waves_per_cu = 8)
 {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         cus = 256;
-    return 8 * (int64_t)cus;
+    return waves_per_cu * (int64_t)cus;
 }
+
+// Units the unit-balanced plan charges per 128 sink + tail tokens: the MFMA
+// kernel's FP16 path against one page of the same pair.
+#ifndef KITTY_FP16_WEIGHT_GQ4
+#define KITTY_FP16_WEIGHT_GQ4 8
+#endif
+#ifndef KITTY_FP16_WEIGHT_GQ8
+#define KITTY_FP16_WEIGHT_GQ8 8
+#endif
+#ifndef KITTY_FP16_WEIGHT_GQ16
+#define KITTY_FP16_WEIGHT_GQ16 8
+#endif
+static int fp16_weight(int GQ)
+{
+    return GQ <= 4 ? KITTY_FP16_WEIGHT_GQ4 : (GQ <= 8 ? KITTY_FP16_WEIGHT_GQ8 : KITTY_FP16_WEIGHT_GQ16);
+}
+constexpr int kMinChunk = 4;  // fewest units per wave of the unit-balanced plan
+#ifndef KITTY_PAGE_WAVES_16THS
+#define KITTY_PAGE_WAVES_16THS 16
+#endif
 
 // Split size.  Every (b, kh) pair gets n_splits page splits plus one FP16
 // split; when the batch allows it, the total is kept within one resident
@@ -39,6 +61,35 @@ static int choose_pages_per_split(const kitty_decode_args &a, int n_fp16)
     if (pps < 4)
         pps = 4;
     return (int)(pps > kMaxPagesPerSplit ? kMaxPagesPerSplit : pps);
+}
+
+// Work plan: the MFMA kernel's unit-balanced plan (pages_per_split > 0
+// asks for at least that many units per wave) or the uniform split plan of
+// the generic kernel.
+static void set_plan(DecodeParams &p, const kitty_decode_args &a, bool balanced)
+{
+    p.balanced = balanced ? 1 : 0;
+    p.n_fp16 = 1;
+    if (!balanced) {
+        p.pages_per_split = choose_pages_per_split(a, p.n_fp16);
+        p.n_splits = (a.max_pages + p.pages_per_split - 1) / p.pages_per_split;
+        p.page_waves = p.min_chunk = p.fp16_weight = p.fp16_units = 0;
+        return;
+    }
+    p.pages_per_split = p.n_splits = 0;
+    p.fp16_weight = fp16_weight(p.GQ);
+    p.fp16_units = seq_fp16_units(p.sink_cap + p.tail_cap, p.fp16_weight);
+    const int64_t res = resident_waves(p.GQ <= 8 ? 8 : 4);
+    if (a.pages_per_split > 0) {
+        p.min_chunk = a.pages_per_split;
+        const int64_t pairs = (int64_t)a.batch * a.num_kv_heads;
+        const int64_t umax = (int64_t)a.max_pages + p.fp16_units + 1;
+        const int64_t waves = pairs * ((umax + p.min_chunk - 1) / p.min_chunk);
+        p.page_waves = (int)(waves < 1 ? 1 : (waves > 16 * res ? 16 * res : waves));
+    } else {
+        p.min_chunk = kMinChunk;
+        p.page_waves = (int)(res * KITTY_PAGE_WAVES_16THS / 16);
+    }
 }
 
 static int build_params(const kitty_decode_args *args, DecodeParams &p)
@@ -93,21 +144,27 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
     p.Dk = a.d_boost;
     p.max_pages = a.max_pages;
     p.flags = a.flags;
-    // FP16 sinks + tail: one split per GQA group of 4 query heads in the MFMA
-    // kernel (its VALU FP16 path costs grow with the group), one otherwise.
-    p.n_fp16 = 1;
-    if (mfma_path_supported(p) && p.GQ > 4)
-        p.n_fp16 = p.GQ / 4;
-    p.pages_per_split = choose_pages_per_split(a, p.n_fp16);
-    p.n_splits = (a.max_pages + p.pages_per_split - 1) / p.pages_per_split;
     p.sm_scale = a.sm_scale;
+    set_plan(p, a, mfma_path_supported(p));
     return KITTY_OK;
+}
+
+// Partial rows of the workspace: uniform plan B * Hq * (n_splits + 1);
+// unit-balanced plan GQ per partial t < 2 (page_waves + pairs).
+static size_t workspace_rows(const DecodeParams &p)
+{
+    if (p.balanced)
+        return 2 * ((size_t)p.page_waves + (size_t)p.B * p.Hkv) * p.GQ;
+    return (size_t)p.B * p.Hq * num_partials(p);
 }
 
 static size_t workspace_bytes(const DecodeParams &p)
 {
-    const size_t rows = (size_t)p.B * p.Hq * num_partials(p);
-    return rows * p.D * sizeof(float) + rows * 2 * sizeof(float);
+    const size_t rows = workspace_rows(p);
+    size_t n = rows * p.D * sizeof(float) + rows * 2 * sizeof(float);
+    if (p.balanced)
+        n += (size_t)p.B * p.Hkv * 2 * sizeof(int);
+    return n;
 }
 
 } // namespace kitty
@@ -126,7 +183,14 @@ extern "C" int kitty_decode_workspace_size(const kitty_decode_args *args, size_t
         return rc;
     if (!bytes)
         return fail(KITTY_E_INVALID, "bytes is NULL");
-    *bytes = workspace_bytes(p);
+    // the size must not depend on which kernel the real pointers select
+    size_t n = workspace_bytes(p);
+    if (mfma_shape_supported(p)) {
+        DecodeParams o = p;
+        set_plan(o, *args, !p.balanced);
+        n = std::max(n, workspace_bytes(o));
+    }
+    *bytes = n;
     return KITTY_OK;
 }
 
@@ -143,7 +207,8 @@ static int prepare(const kitty_decode_args *args, DecodeParams &p)
     if ((uintptr_t)args->workspace & 15)
         return fail(KITTY_E_INVALID, "workspace must be 16-byte aligned");
     p.ws_o = (float *)args->workspace;
-    p.ws_ml = p.ws_o + (size_t)p.B * p.Hq * num_partials(p) * p.D;
+    p.ws_ml = p.ws_o + workspace_rows(p) * p.D;
+    p.ws_pair = (int *)(p.ws_ml + workspace_rows(p) * 2);
     return KITTY_OK;
 }
 

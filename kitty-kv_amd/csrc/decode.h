@@ -28,19 +28,65 @@ struct DecodeParams {
     int sink_cap, tail_cap;
     int B, Hq, Hkv, GQ, D, G, Dk;
     int max_pages, pages_per_split, n_splits;
-    int n_fp16;   // FP16 splits per (b, kh): each takes an equal share of the sink + tail tokens
+    int n_fp16;   // FP16 splits per (b, kh) of the uniform plan (one)
     int flags;
     float sm_scale;
-    float *ws_o;  // [B][Hq][n_splits + 1][D] unnormalised partial outputs
-    float *ws_ml; // [B][Hq][n_splits + 1][2] running max (log2 domain) and sum
+    // Unit-balanced plan of the MFMA kernel (balanced = 1): the grid has
+    // page_waves waves, each at least min_chunk units; fp16_weight = units
+    // charged per 128 sink + tail tokens.
+    int balanced, page_waves, min_chunk, fp16_weight;
+    int fp16_units;  // FP16 units per pair: seq_fp16_units(sink_cap + tail_cap, fp16_weight)
+    float *ws_o;  // uniform: [B][Hq][num_partials][D]; balanced: [partial t][GQ][D]
+    float *ws_ml; // the same rows: running max (log2 domain) and sum
+    int *ws_pair; // balanced: [B * Hkv][2] first and last partial t of each (b, kh)
 };
 
-// Partials per (b, query head): page splits, then FP16 splits.
+// Partials per (b, query head) of the uniform plan: page splits, then FP16 splits.
 __host__ __device__ inline int num_partials(const DecodeParams &p) { return p.n_splits + p.n_fp16; }
+
+// ---------------------------------------------------------------------------
+// Unit-balanced plan (MFMA kernel).  Sequence b owns page units (one per
+// page) followed by FP16 units (fp16_units, for the sink + tail tokens); its Hkv pairs (b, kh) each own that many consecutive
+// units, pairs in order j = b * Hkv + kh.  Wave w of the W working waves
+// takes units [floor(w U / W), floor((w + 1) U / W)) of the U in all, so every
+// wave gets the same work whatever the context lengths, and writes one
+// partial per (pair, part) it touches: partial t = w + 2 j + part (part 0
+// pages, 1 FP16), which increases strictly along the unit order, so t is
+// unique and t < 2 (W + pairs).  The wave that starts pair j stores its t as
+// ws_pair[2 j], the wave that ends it as ws_pair[2 j + 1]; every partial in
+// between belongs to pair j.  The one slot in that range no wave computes (a
+// wave boundary exactly between the pair's pages and its FP16 tokens) is
+// written empty by the wave before it.
+
+// Page units of a sequence: its pages; one unit (which reports NaN) for an
+// invalid page count; one empty unit for a sequence with no pages when the
+// pairs own no FP16 units, so every pair owns a partial.
+__host__ __device__ inline int seq_page_units(int np_raw, int max_pages, int fp16_units)
+{
+    if (np_raw < 0 || np_raw > max_pages)
+        return 1;
+    return np_raw > 0 ? np_raw : (fp16_units > 0 ? 0 : 1);
+}
+// FP16 units of every pair: the sink + tail capacity, fp16_weight units per
+// 128 tokens (the tokens a sequence actually holds are split evenly over
+// them), so the plan depends on the page counts alone.
+__host__ __device__ inline int seq_fp16_units(int ntok, int weight)
+{
+    return ntok > 0 ? (int)(((int64_t)ntok * weight + 127) / 128) : 0;
+}
+// working waves for U units: at most page_waves, each at least min_chunk units
+__host__ __device__ inline int plan_waves(int64_t U, int page_waves, int min_chunk)
+{
+    if (U >= (int64_t)page_waves * min_chunk)
+        return page_waves;
+    const int w = (int)((uint32_t)U / (uint32_t)min_chunk);  // U < 2^31 here
+    return w < 1 ? 1 : w;
+}
 
 size_t generic_lds_bytes(int GQ, int D, int G, int Dk);
 int launch_generic(const DecodeParams &p, hipStream_t stream);
 int launch_splits(const DecodeParams &p, hipStream_t stream);
+bool mfma_shape_supported(const DecodeParams &p);
 bool mfma_path_supported(const DecodeParams &p);
 int launch_mfma(const DecodeParams &p, hipStream_t stream);
 int launch_merge(const DecodeParams &p, hipStream_t stream);

@@ -1,14 +1,16 @@
 // Split-K paged decode attention over Kitty's dense-sparse pages (gfx950).
 //
-// Work decomposition (flash-decoding): for every (sequence b, KV head kh) the
-// quantised pages are cut into splits of `pages_per_split` pages; `n_fp16`
-// extra splits per (b, kh) attend the FP16 sinks and tail, each an equal
-// share of their tokens.  Each split produces,
-// for every query head of the GQA group, an unnormalised partial
-// (O, m, l) in base-2 online-softmax form; a merge kernel combines the
-// num_partials partials of (b, qh) into the fp16 output.  The result equals
-// softmax(q K^T / sqrt(D)) V over sinks ‖ dequantised pages ‖ tail, which is
-// paged_attention_reference (kitty/kernels/attention.py:136-189).
+// Work decomposition (flash-decoding).  Uniform plan (the generic kernel of
+// this file): for every (sequence b, KV head kh) the quantised pages are cut
+// into splits of `pages_per_split` pages, plus one split for the FP16 sinks
+// and tail.  Unit-balanced plan (the MFMA kernel, decode_mfma.hip): every
+// wave takes an equal share of all (pair, page) and FP16 units, one partial
+// per pair it touches.  Each split or segment produces, for every query head
+// of the GQA group, an unnormalised partial (O, m, l) in base-2 online-softmax
+// form; the merge kernel below combines the partials of (b, qh) into the fp16
+// output.  The result equals softmax(q K^T / sqrt(D)) V over sinks ‖
+// dequantised pages ‖ tail, which is paged_attention_reference
+// (kitty/kernels/attention.py:136-189).
 //
 // This file holds the shape-generic path (any D, G <= 256, multiples of 4):
 // pages are staged in LDS and dequantised with the reference's own formula
@@ -285,27 +287,98 @@ __device__ __forceinline__ float wave_sum(float v)
     return v;
 }
 
+// Merge of NS <= N partials (N <= 128; rows row0 + s * rstep) in one round
+// trip: lane l holds (m, l) of partials l and l + 64, every lane loads the N
+// O rows of its channel pair (rows past NS repeat the last, with weight 0).
+template <int N>
+__device__ __forceinline__ void merge_one_pass(const DecodeParams &p, int64_t row0, int64_t rstep, int NS, uint16_t *o)
+{
+    static_assert(N <= 128, "two partials per lane at most");
+    const int lane = threadIdx.x;
+    const float ninf = -__builtin_inff();
+    const int d = 2 * lane;
+    const int dd = d < p.D ? d : p.D - 2;  // D is a multiple of 4: d < D implies d + 1 < D
+    const float2 ml0 = *(const float2 *)(p.ws_ml + 2 * (row0 + min(lane, NS - 1) * rstep));
+    float2 ml1 = make_float2(ninf, 0.0f);
+    if (N > 64)
+        ml1 = *(const float2 *)(p.ws_ml + 2 * (row0 + min(64 + lane, NS - 1) * rstep));
+    float2 v[N];
+#pragma unroll
+    for (int u = 0; u < N; ++u)
+        v[u] = *(const float2 *)(p.ws_o + (row0 + min(u, NS - 1) * rstep) * p.D + dd);
+    const bool in0 = lane < NS, in1 = N > 64 && 64 + lane < NS;
+    const float M = wave_max(fmaxf(in0 ? ml0.x : ninf, in1 ? ml1.x : ninf));
+    const bool nan = wave_max((in0 && ml0.x != ml0.x) || (in1 && ml1.x != ml1.x) ? 1.0f : 0.0f) > 0.0f;
+    const float w0 = in0 && ml0.x != ninf && M != ninf ? exp2f(ml0.x - M) : 0.0f;
+    const float w1 = in1 && ml1.x != ninf && M != ninf ? exp2f(ml1.x - M) : 0.0f;
+    const float L = wave_sum(w0 * ml0.y + w1 * ml1.y);
+    float ax = 0.0f, ay = 0.0f;
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+        const float wl = u < 64 ? w0 : w1;
+        const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), u & 63));
+        ax += wu * v[u].x;
+        ay += wu * v[u].y;
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;  // no tokens -> zeros (attention.py:180-182)
+    if (d < p.D) {
+        const float x = nan ? __builtin_nanf("") : ax * inv, y = nan ? __builtin_nanf("") : ay * inv;
+        if (((uintptr_t)o & 3) == 0) {
+            *(uint32_t *)(o + d) = (uint32_t)f2h(x) | ((uint32_t)f2h(y) << 16);
+        } else {
+            o[d] = f2h(x);
+            o[d + 1] = f2h(y);
+        }
+    }
+}
+
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
 {
     constexpr int kBatch = 32;
+    constexpr int kOnePass = 128;  // partials merged in one round trip (two per lane)
     const int lane = threadIdx.x;
     const int bq = blockIdx.x;
     const int b = bq / p.Hq, qh = bq - b * p.Hq;
-    const int NS = num_partials(p);
-    const int64_t row0 = (int64_t)bq * NS;
+    // Partials of this query head: NS rows from row0, step rstep apart
+    // (uniform plan: consecutive rows; unit-balanced plan: partials t_first ..
+    // t_last of its (b, kh) pair, GQ rows per partial).
+    int NS = num_partials(p);
+    int64_t row0 = (int64_t)bq * NS, rstep = 1;
+    if (p.balanced) {
+        const int j = b * p.Hkv + qh / p.GQ;
+        const int t0 = p.ws_pair[2 * j], t1 = p.ws_pair[2 * j + 1];
+        NS = t1 - t0 + 1;
+        row0 = (int64_t)t0 * p.GQ + qh % p.GQ;
+        rstep = p.GQ;
+    }
     const float ninf = -__builtin_inff();
+    uint16_t *o = p.out + b * p.out_s_seq + qh * p.out_s_head;
+
+    // At most 128 partials and D <= 128 (the usual case): one round trip,
+    // every (m, l) and O row loaded together, the max taken over the batch.
+    if (NS <= 32 && p.D <= 128) {
+        merge_one_pass<32>(p, row0, rstep, NS, o);
+        return;
+    }
+    if (NS <= 64 && p.D <= 128) {
+        merge_one_pass<64>(p, row0, rstep, NS, o);
+        return;
+    }
+    if (NS <= kOnePass && p.D <= 128) {
+        merge_one_pass<kOnePass>(p, row0, rstep, NS, o);
+        return;
+    }
 
     float M = ninf;
     int nan = 0;
     for (int s = lane; s < NS; s += 64) {
-        const float m = p.ws_ml[2 * (row0 + s)];
+        const float m = p.ws_ml[2 * (row0 + s * rstep)];
         nan |= m != m;
         M = fmaxf(M, m);
     }
     M = wave_max(M);
     nan = wave_max((float)nan) > 0.0f;
 
-    uint16_t *o = p.out + b * p.out_s_seq + qh * p.out_s_head;
     float L = 0.0f;
     for (int d0 = 0; d0 < p.D; d0 += 128) {
         const int d = d0 + 2 * lane;            // D is a multiple of 4: d < D implies d + 1 < D
@@ -313,11 +386,11 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
         float ax = 0.0f, ay = 0.0f, lsum = 0.0f;
         for (int s0 = 0; s0 < NS; s0 += kBatch) {
             const int sl = min(s0 + lane, NS - 1);
-            const float2 ml = *(const float2 *)(p.ws_ml + 2 * (row0 + sl));
+            const float2 ml = *(const float2 *)(p.ws_ml + 2 * (row0 + sl * rstep));
             float2 v[kBatch];
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
-                const int64_t row = row0 + min(s0 + u, NS - 1);
+                const int64_t row = row0 + min(s0 + u, NS - 1) * rstep;
                 v[u] = *(const float2 *)(p.ws_o + row * p.D + dd);
             }
             const bool live = lane < kBatch && s0 + lane < NS && ml.x != ninf && M != ninf;

@@ -245,110 +245,130 @@ __device__ __forceinline__ void wait_vmcnt()
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// FP16 sinks and tail of (b, kh), one wave, VALU.  Chunks of 64 tokens: lane
-// t scores token t for every head (its K row read as 16 independent 16-byte
-// loads), then lane l accumulates channels 2l, 2l+1 over the chunk, reading
-// 16 value rows per batch of independent loads.
+// Sink + tail tokens [lo, hi) of pair (b, kh) (sink tokens first), 32 per
+// step.  The step's K and V rows stream into the two LDS stages with
+// global_load_lds (no registers hold data in flight): K chunk c of token row n
+// is stored at chunk c ^ (n & 15), so the 16 rows one MFMA B read touches hit
+// 16 different bank groups.  QK: f16 MFMAs with the heads on rows (A = q *
+// sm_scale * log2(e) in fp16, B = K rows), base-2 online softmax per head row
+// with DPP row reductions, P through LDS.  PV: VALU, lane = channel pair.
+// Returns each head's (m, l) and O (channels 2 lane, 2 lane + 1).
 template <int GQ>
-__device__ void fp16_segments(const DecodeParams &p, int b, int kh, int part, float *qs, float *pb, float *m_out,
-                              float *l_out, float (*O)[2])
+__device__ void fp16_segments(const DecodeParams &p, int b, int kh, int lo, int hi, unsigned char *kst,
+                              unsigned char *vst, float *m_out, float *l_out, float (*O)[2])
 {
-    const int lane = threadIdx.x;
-    const float qscale = p.sm_scale * kLog2e;
-    for (int e = lane; e < GQ * 128; e += 64)
-        qs[e] = h2f(p.q[b * p.q_s_seq + (int64_t)(kh * GQ + e / 128) * p.q_s_head + (e & 127)]) * qscale;
-    float m[GQ], l[GQ];
+    constexpr int kTok = 32;
+    const int lane = threadIdx.x, r = lane & 15, kq = lane >> 4;
+    float *pbuf = (float *)(vst + kTok * 256);  // [head][token] fp32, GQ * 32 floats
+    // A operand: row r = head r (rows past GQ are zero), k = 8 kq + i of each
+    // 32-channel step
+    half8 qa[4];
+    {
+        const float qscale = p.sm_scale * kLog2e;
+        const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + (r < GQ ? r : 0)) * p.q_s_head;
 #pragma unroll
-    for (int g = 0; g < GQ; ++g) {
-        m[g] = -__builtin_inff();
-        l[g] = 0.0f;
-        O[g][0] = O[g][1] = 0.0f;
-    }
-    __syncthreads();
-    const int ns = min(max(0, p.sink_len[b]), p.sink_cap), nt = min(max(0, p.tail_len[b]), p.tail_cap);
-    // this split's share of the concatenated sink + tail tokens
-    const int lo = (int)((int64_t)(ns + nt) * part / p.n_fp16), hi = (int)((int64_t)(ns + nt) * (part + 1) / p.n_fp16);
-    for (int seg = 0; seg < 2; ++seg) {
-        const kitty_fp16_seg &K = seg == 0 ? p.sink_k : p.tail_k;
-        const kitty_fp16_seg &V = seg == 0 ? p.sink_v : p.tail_v;
-        const int base = seg == 0 ? 0 : ns;
-        const int s0 = max(lo - base, 0), s1 = min(hi - base, seg == 0 ? ns : nt);
-        const uint16_t *kb = K.ptr + b * K.s_seq + kh * K.s_head;
-        const uint16_t *vb = V.ptr + b * V.s_seq + kh * V.s_head;
-        for (int c0 = s0; c0 < s1; c0 += 64) {
-            const int cnt = min(64, s1 - c0);
-            const uint16_t *row = kb + (int64_t)(c0 + min(lane, cnt - 1)) * K.s_tok;
-            float sc[GQ];
+        for (int s = 0; s < 4; ++s) {
+            const u32x4 raw = *(const u32x4 *)(qrow + 32 * s + 8 * kq);
+            u32x4 v;
 #pragma unroll
-            for (int g = 0; g < GQ; ++g)
-                sc[g] = 0.0f;
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                u32x4 kr[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    kr[i] = *(const u32x4 *)(row + 64 * hf + 8 * i);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    float kv[8];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const half2v h = as_h2(kr[i][e]);
-                        kv[2 * e] = (float)h[0];
-                        kv[2 * e + 1] = (float)h[1];
-                    }
-#pragma unroll
-                    for (int g = 0; g < GQ; ++g) {
-                        const float4 q0 = *(const float4 *)(qs + g * 128 + 64 * hf + 8 * i);
-                        const float4 q1 = *(const float4 *)(qs + g * 128 + 64 * hf + 8 * i + 4);
-                        sc[g] += q0.x * kv[0] + q0.y * kv[1] + q0.z * kv[2] + q0.w * kv[3] + q1.x * kv[4] +
-                                 q1.y * kv[5] + q1.z * kv[6] + q1.w * kv[7];
-                    }
-                }
+            for (int j = 0; j < 4; ++j) {
+                const half2v h = as_h2(raw[j]);
+                v[j] = r < GQ ? pack_h2((float)h[0] * qscale, (float)h[1] * qscale) : 0u;
             }
-#pragma unroll
-            for (int g = 0; g < GQ; ++g) {
-                const float s = lane < cnt ? sc[g] : -__builtin_inff();
-                float mx = s;
-                for (int off = 32; off > 0; off >>= 1)
-                    mx = fmaxf(mx, __shfl_xor(mx, off));
-                const float mn = fmaxf(m[g], mx);
-                const float alpha = __builtin_amdgcn_exp2f(m[g] - mn);
-                const float pr = lane < cnt ? __builtin_amdgcn_exp2f(s - mn) : 0.0f;
-                float sum = pr;
-                for (int off = 32; off > 0; off >>= 1)
-                    sum += __shfl_xor(sum, off);
-                l[g] = l[g] * alpha + sum;
-                m[g] = mn;
-                O[g][0] *= alpha;
-                O[g][1] *= alpha;
-                pb[g * 64 + lane] = pr;
-            }
-            __syncthreads();
-            for (int t0 = 0; t0 < cnt; t0 += 16) {
-                unsigned vv[16];
-#pragma unroll
-                for (int j = 0; j < 16; ++j)
-                    vv[j] = *(const unsigned *)(vb + (int64_t)(c0 + min(t0 + j, cnt - 1)) * V.s_tok + 2 * lane);
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const half2v h = as_h2(vv[j]);
-                    const float v0 = (float)h[0], v1 = (float)h[1];
-#pragma unroll
-                    for (int g = 0; g < GQ; ++g) {
-                        const float w = t0 + j < cnt ? pb[g * 64 + t0 + j] : 0.0f;
-                        O[g][0] += w * v0;
-                        O[g][1] += w * v1;
-                    }
-                }
-            }
-            __syncthreads();
+            qa[s] = __builtin_bit_cast(half8, v);
         }
     }
+    float m[4], l[4];  // head rows 4 kq + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m[i] = -__builtin_inff();
+        l[i] = 0.0f;
+    }
+#pragma unroll
+    for (int g = 0; g < GQ; ++g)
+        O[g][0] = O[g][1] = 0.0f;
+    const int ns = min(max(0, p.sink_len[b]), p.sink_cap);
+    const uint16_t *sk = p.sink_k.ptr + b * p.sink_k.s_seq + kh * p.sink_k.s_head;
+    const uint16_t *sv = p.sink_v.ptr + b * p.sink_v.s_seq + kh * p.sink_v.s_head;
+    const uint16_t *tk = p.tail_k.ptr + b * p.tail_k.s_seq + kh * p.tail_k.s_head;
+    const uint16_t *tv = p.tail_v.ptr + b * p.tail_v.s_seq + kh * p.tail_v.s_head;
+    for (int c0 = lo; c0 < hi; c0 += kTok) {
+        const int cnt = min(kTok, hi - c0);
+        // ---- 16 direct-to-LDS loads: instruction i covers rows 4i .. 4i+3
+#pragma unroll
+        for (int i = 0; i < kTok / 4; ++i) {
+            const int n = 4 * i + kq;                 // token row of this lane's slot
+            const int tt = c0 + min(n, cnt - 1);      // rows past cnt repeat the last token
+            const bool sink = tt < ns;
+            const uint16_t *krow = sink ? sk + (int64_t)tt * p.sink_k.s_tok : tk + (int64_t)(tt - ns) * p.tail_k.s_tok;
+            const uint16_t *vrow = sink ? sv + (int64_t)tt * p.sink_v.s_tok : tv + (int64_t)(tt - ns) * p.tail_v.s_tok;
+            gll16((const unsigned char *)(krow + 8 * (r ^ (n & 15))), kst + 1024 * i);
+            gll16((const unsigned char *)(vrow + 8 * r), vst + 1024 * i);
+        }
+        wait_vmcnt<0>();
+        // ---- QK: tile tg covers tokens 16 tg + r; S[tg][i] = head 4 kq + i
+        f32x4 S[2];
+#pragma unroll
+        for (int tg = 0; tg < 2; ++tg) {
+            S[tg] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const int n = 16 * tg + r;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const half8 kb = *(const half8 *)(kst + 256 * n + 16 * ((4 * s + kq) ^ r));
+                S[tg] = mfma(qa[s], kb, S[tg]);
+            }
+        }
+        // ---- online softmax per head row (tokens past cnt masked)
+        float alpha[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float s0 = r < cnt ? S[0][i] : -__builtin_inff();
+            const float s1 = 16 + r < cnt ? S[1][i] : -__builtin_inff();
+            const float mx = row_max16(fmaxf(s0, s1));
+            const float mn = fmaxf(m[i], mx);
+            alpha[i] = __builtin_amdgcn_exp2f(m[i] - mn);
+            const float p0 = __builtin_amdgcn_exp2f(s0 - mn), p1 = __builtin_amdgcn_exp2f(s1 - mn);
+            l[i] = l[i] * alpha[i] + row_sum16(p0 + p1);
+            m[i] = mn;
+            const int h = 4 * kq + i;
+            if (h < GQ) {
+                pbuf[h * kTok + r] = p0;
+                pbuf[h * kTok + 16 + r] = p1;
+            }
+        }
+        __syncthreads();
+        // ---- PV: lane = channels 2 lane, 2 lane + 1
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+            const float al = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha[g & 3]), 16 * (g >> 2)));
+            O[g][0] *= al;
+            O[g][1] *= al;
+        }
+#pragma unroll
+        for (int t4 = 0; t4 < kTok / 4; ++t4) {
+            unsigned vv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                vv[e] = *(const unsigned *)(vst + 256 * (4 * t4 + e) + 4 * lane);
+#pragma unroll
+            for (int g = 0; g < GQ; ++g) {
+                const float4 w = *(const float4 *)(pbuf + g * kTok + 4 * t4);
+                const float wt[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const half2v h = as_h2(vv[e]);
+                    O[g][0] += wt[e] * (float)h[0];
+                    O[g][1] += wt[e] * (float)h[1];
+                }
+            }
+        }
+        __syncthreads();  // LDS reads done before the next step's loads land
+    }
 #pragma unroll
     for (int g = 0; g < GQ; ++g) {
-        m_out[g] = m[g];
-        l_out[g] = l[g];
+        m_out[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m[g & 3]), 16 * (g >> 2)));
+        l_out[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l[g & 3]), 16 * (g >> 2)));
     }
 }
 
@@ -489,7 +509,10 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     constexpr int HPL = GQ / 4;
     constexpr int RSTEP = 4 / HPL;  // accumulator register of head slot j = j * RSTEP
     const int q = lane >> 4, r = lane & 15;
-    const half8 neg1024 = __builtin_bit_cast(half8, u32x4{0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u});
+    // materialised per page (4 moves): held across the page loop it is spilled
+    u32x4 n1024 = {0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u};
+    asm volatile("" : "+v"(n1024));
+    const half8 neg1024 = __builtin_bit_cast(half8, n1024);
 
     const CodeMasks &cm = W.cm;
 
@@ -684,44 +707,60 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     __builtin_amdgcn_s_setprio(0);
 }
 
-// Occupancy target (waves per SIMD): two waves for GQA groups of 4 and 8
-// (256 registers each, measured faster than one wave with no register cap),
-// one for 16 heads, whose accumulators do not fit in 256.
+// Global loads that start a page segment of pair (b, kh): boost_idx of the
+// lane's two channels, the lane's slice of the q rows and the ids of pages
+// p0 .. p0 + 63 (below p1).  Issued by the caller, so the kernel can start
+// them for its first segment before its plan is known.
+struct SegSetup {
+    int bi0, bi1;
+    u32x4 qraw[4];
+    int ids;
+};
+
 template <int GQ>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(GQ <= 8 ? 2 : 1)))
-void decode_mfma_kernel(DecodeParams p)
+__device__ __forceinline__ SegSetup load_setup(const DecodeParams &p, int b, int kh, int p0, int p1)
+{
+    constexpr int ROWS_PER_HEAD = 16 / GQ;
+    const int lane = threadIdx.x, q = lane >> 4, r = lane & 15;
+    SegSetup s;
+    s.bi0 = p.boost_idx[kh * 128 + lane];
+    s.bi1 = p.boost_idx[kh * 128 + 64 + lane];
+    const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + r / ROWS_PER_HEAD) * p.q_s_head;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        s.qraw[i] = *(const u32x4 *)(qrow + 32 * i + 8 * q);
+    s.ids = p0 + lane < min(p1, p.max_pages) ? p.block_table[b * p.bt_stride + p0 + lane] : 0;
+    return s;
+}
+
+// Pages [p0, p1) of pair (b, kh) folded into partial t: row t * GQ + h
+// holds query head kh * GQ + h.  A page count outside [0, max_pages] or a
+// page id outside the pool makes the partial NaN; no pages leave an empty
+// partial (m = -inf, l = 0, O = 0).
+template <int GQ>
+__device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned char *stage0, unsigned char *stage1,
+                                             int b, int kh, int np_raw, int p0, int p1, int64_t t, const SegSetup &su)
 {
     constexpr int HPL = GQ / 4;
     constexpr int RSTEP = 4 / HPL;
     constexpr int ROWS_PER_HEAD = 16 / GQ;
-    // Two LDS stages: the wave computes on one while the next page streams
-    // into the other with global_load_lds.
-    __shared__ __attribute__((aligned(16))) unsigned char stage0[kStage];
-    __shared__ __attribute__((aligned(16))) unsigned char stage1[kStage];
-
-    const int lane = threadIdx.x, q = lane >> 4, r = lane & 15;
-    const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
-    const int NS = num_partials(p);
-
-    if (split >= p.n_splits) {
-        float m[GQ], l[GQ], O[GQ][2];
-        fp16_segments<GQ>(p, b, kh, split - p.n_splits, (float *)stage0, (float *)stage1, m, l, O);
-        for (int g = 0; g < GQ; ++g) {
-            const int64_t row = ((int64_t)b * p.Hq + kh * GQ + g) * NS + split;
-            *(float2 *)(p.ws_o + row * 128 + 2 * lane) = make_float2(O[g][0], O[g][1]);
-            if (lane == 0) {
-                p.ws_ml[2 * row] = m[g];
-                p.ws_ml[2 * row + 1] = l[g];
-            }
-        }
-        return;
-    }
-
+    // lane-derived offsets are rebuilt per segment (the asm hides the lane
+    // id): kept across the caller's segment loop they would be spilled
+    int lane = threadIdx.x;
+    asm volatile("" : "+v"(lane));
+    const int q = lane >> 4, r = lane & 15;
     const int Dk = p.Dk;
-    const int np = p.num_pages[b];
-    bool poison = np < 0 || np > p.max_pages;
-    const int p0 = split * p.pages_per_split;
-    const int p1 = poison ? p0 : min(np, p0 + p.pages_per_split);
+    // segment bounds come out of VALU divisions: keep the loop control scalar
+    b = __builtin_amdgcn_readfirstlane(b);
+    kh = __builtin_amdgcn_readfirstlane(kh);
+    np_raw = __builtin_amdgcn_readfirstlane(np_raw);
+    p0 = __builtin_amdgcn_readfirstlane(p0);
+    p1 = __builtin_amdgcn_readfirstlane(p1);
+    bool poison = np_raw < 0 || np_raw > p.max_pages;
+    if (poison)
+        p1 = p0;
+    else if (p1 > np_raw)
+        p1 = np_raw;
 
     // rank -> channel map of this KV head (inverse of boost_idx), built in
     // stage1 before any page lands there.
@@ -729,11 +768,10 @@ void decode_mfma_kernel(DecodeParams p)
     if (lane < 32)
         rank_chan[lane] = 0;
     __syncthreads();
-    for (int d = lane; d < 128; d += 64) {
-        const int bi = p.boost_idx[kh * 128 + d];
-        if (bi < Dk)
-            rank_chan[bi] = d;
-    }
+    if (su.bi0 < Dk)
+        rank_chan[su.bi0] = lane;
+    if (su.bi1 < Dk)
+        rank_chan[su.bi1] = 64 + lane;
     __syncthreads();
 
     WaveState<GQ> W;
@@ -746,10 +784,7 @@ void decode_mfma_kernel(DecodeParams p)
     const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + hr) * p.q_s_head;
     const float qscale = head_row ? p.sm_scale * kLog2e : 0.0f;
     {
-        u32x4 qraw[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-            qraw[s] = *(const u32x4 *)(qrow + 32 * s + 8 * q);
+        const u32x4 *qraw = su.qraw;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             W.hch[i] = rank_chan[8 * q + i];
@@ -806,12 +841,24 @@ void decode_mfma_kernel(DecodeParams p)
         W.o4[ch][0] = W.o4[ch][1] = 0.0f;
     __syncthreads();  // rank_chan reads done before stage1 is overwritten
 
-    // Page ids of this split (at most 64, see choose_pages_per_split), one
-    // per lane, loaded once and read back with v_readlane so no page waits on
-    // a dependent global load.
-    const int ids = p0 + lane < p1 ? p.block_table[b * p.bt_stride + p0 + lane] : 0;
+    // Page ids, 64 at a time (one per lane), read back with v_readlane so no
+    // page waits on a dependent global load; pages are asked for in order,
+    // so the next 64 ids are fetched when the first page past them is.  That
+    // fetch waits for itself at once (and for the page in flight, once per 64
+    // pages): left pending, it would make the compiler wait for every
+    // outstanding load before each page's v_readlane.
+    const int32_t *bt = p.block_table + b * p.bt_stride;
+    int chunk0 = p0;
+    int ids = su.ids;
     auto page_ok = [&](int32_t page) { return page >= 0 && page < p.num_pool_pages; };
-    auto page_at = [&](int pi) -> int32_t { return __builtin_amdgcn_readlane(ids, pi - p0); };
+    auto page_at = [&](int pi) -> int32_t {
+        if (pi - chunk0 >= 64) {
+            chunk0 += 64;
+            ids = chunk0 + lane < p1 ? bt[chunk0 + lane] : 0;
+            wait_vmcnt<0>();
+        }
+        return __builtin_amdgcn_readlane(ids, pi - chunk0);
+    };
 
     if (p0 < p1) {
         const int32_t page = page_at(p0);
@@ -868,7 +915,7 @@ void decode_mfma_kernel(DecodeParams p)
     for (int j = 0; j < HPL; ++j) {
         const float l = row_sum16(W.l_run[j]);
         const int h = q * HPL + j;
-        const int64_t row = ((int64_t)b * p.Hq + kh * GQ + h) * NS + split;
+        const int64_t row = t * GQ + h;
         float *o = p.ws_o + row * 128;
         if constexpr (GQ == 4) {
             // o4[ch][e] is O of channel 32ch + 2r + e
@@ -897,14 +944,280 @@ void decode_mfma_kernel(DecodeParams p)
     }
 }
 
+// Empty partial t (m = -inf, l = 0, O = 0) for the slot between a pair's
+// pages and its FP16 tokens when a wave boundary falls exactly there.
+template <int GQ>
+__device__ __forceinline__ void empty_partial(const DecodeParams &p, int64_t t)
+{
+    const int lane = threadIdx.x;
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+        const int64_t row = t * GQ + g;
+        *(float2 *)(p.ws_o + row * 128 + 2 * lane) = make_float2(0.0f, 0.0f);
+        if (lane == 0) {
+            p.ws_ml[2 * row] = -__builtin_inff();
+            p.ws_ml[2 * row + 1] = 0.0f;
+        }
+    }
+}
+
+// Inclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane)
+{
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(v, off);
+        if (lane >= off)
+            v += y;
+    }
+    return v;
+}
+
+__device__ __forceinline__ int64_t uniform64(int64_t v)
+{
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ int seq_tokens(const DecodeParams &p, int b)
+{
+    return min(max(0, p.sink_len[b]), p.sink_cap) + min(max(0, p.tail_len[b]), p.tail_cap);
+}
+
+// Sequence b as the unit plan sees it (all fields wave-uniform).
+struct SeqUnits {
+    int b, np_raw, npu, fu;  // raw page count, page units, FP16 units (per pair)
+    int64_t base;            // first unit of pair (b, 0)
+};
+
+// Units [u0, u1) of wave w: floor(w U / W) = w Q + (w R) / W with Q = U / W,
+// R = U % W (w R < W^2 < 2^32); one 32-bit division when U fits.
+__device__ __forceinline__ void wave_units(int64_t U, int W, int w, int64_t &u0, int64_t &u1)
+{
+    uint64_t Q;
+    uint32_t R;
+    if (U <= 0xffffffffll) {
+        Q = (uint32_t)U / (uint32_t)W;
+        R = (uint32_t)U - (uint32_t)Q * (uint32_t)W;
+    } else {
+        Q = (uint64_t)U / (uint64_t)W;
+        R = (uint32_t)((uint64_t)U - Q * (uint64_t)W);
+    }
+    u0 = (int64_t)(Q * (uint64_t)w + ((uint32_t)w * R) / (uint32_t)W);
+    u1 = (int64_t)(Q * (uint64_t)(w + 1) + ((uint32_t)(w + 1) * R) / (uint32_t)W);
+}
+
+// The kernel's parameters read again from the kernarg segment (pp: the
+// kernel's own __builtin_amdgcn_kernarg_segment_ptr(), which is only defined
+// inside the kernel and so is passed to functions that are not inlined).  The
+// segment loop below calls this in each branch so that only the plan state
+// stays live from one segment to the next; the empty asm hides the pointer's
+// value so the loads cannot be hoisted out of the loop.
+typedef const __attribute__((address_space(4))) DecodeParams *KernargParams;
+__device__ __forceinline__ DecodeParams kernel_params(KernargParams pp)
+{
+    asm volatile("" : "+s"(pp));
+    DecodeParams r;
+    __builtin_memcpy(&r, (const void *)pp, sizeof(r));
+    return r;
+}
+
+// FP16 tokens [lo, hi) of pair (b, kh) as partial t.  Out of line: the page
+// loop's registers need not be kept around it.
+template <int GQ>
+__device__ __forceinline__ void fp16_partial(KernargParams kp, int b, int kh, int lo, int hi, int64_t t,
+                                          unsigned char *stage0, unsigned char *stage1)
+{
+    // arguments arrive in vector registers: the pointer is the same in every lane
+    const uint64_t a = (uint64_t)kp;
+    const uint32_t lo32 = __builtin_amdgcn_readfirstlane((uint32_t)a), hi32 = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    const DecodeParams P = kernel_params((KernargParams)(((uint64_t)hi32 << 32) | lo32));
+    b = __builtin_amdgcn_readfirstlane(b);
+    kh = __builtin_amdgcn_readfirstlane(kh);
+    lo = __builtin_amdgcn_readfirstlane(lo);
+    hi = __builtin_amdgcn_readfirstlane(hi);
+    const int lane = threadIdx.x;
+    float m[GQ], l[GQ], O[GQ][2];
+    fp16_segments<GQ>(P, b, kh, lo, hi, stage0, stage1, m, l, O);
+    for (int g = 0; g < GQ; ++g) {
+        const int64_t row = t * GQ + g;
+        *(float2 *)(P.ws_o + row * 128 + 2 * lane) = make_float2(O[g][0], O[g][1]);
+        if (lane == 0) {
+            P.ws_ml[2 * row] = m[g];
+            P.ws_ml[2 * row + 1] = l[g];
+        }
+    }
+    __syncthreads();  // stage reads done before the next segment reuses them
+}
+
+// Occupancy target (waves per SIMD): two waves for GQA groups of 4 and 8
+// (256 registers each, measured faster than one wave with no register cap),
+// one for 16 heads, whose accumulators do not fit in 256.
+//
+// Wave w works through units [w U / W, (w + 1) U / W) of the unit-balanced
+// plan: a run of pages or of FP16 tokens of one pair per segment, one
+// partial per segment.
+template <int GQ>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(GQ <= 8 ? 2 : 1)))
+void decode_mfma_kernel(DecodeParams p)
+{
+    // Two LDS stages: the wave computes on one while the next page streams
+    // into the other with global_load_lds.
+    __shared__ __attribute__((aligned(16))) unsigned char stage0[kStage];
+    __shared__ __attribute__((aligned(16))) unsigned char stage1[kStage];
+
+    const int lane = threadIdx.x;
+    const KernargParams kp = (KernargParams)__builtin_amdgcn_kernarg_segment_ptr();
+    const int w = blockIdx.x;
+    const int F = p.fp16_units;
+    // ---- the plan's input, page counts 64 sequences per step (issued first)
+    int np_l = 0, units_l = 0;  // sequence b0 + lane of the current step
+    auto load_step = [&](int b0) {
+        const int b = b0 + lane;
+        np_l = b < p.B ? p.num_pages[b] : 0;
+        units_l = b < p.B ? seq_page_units(np_l, p.max_pages, F) + F : 0;
+    };
+    load_step(0);
+    // ---- static plan: every sequence at max_pages.  Its first page segment
+    // is loaded while the page counts are in flight; when the batch turns out
+    // to be that uniform, it is the plan and no scan is needed.
+    const int units_s = seq_page_units(p.max_pages, p.max_pages, F) + F;
+    const int npu_s = units_s - F;
+    const int64_t U_s = (int64_t)p.B * p.Hkv * units_s;
+    const int W_s = plan_waves(U_s, p.page_waves, p.min_chunk);
+    int64_t s0 = 0, s1 = 0;
+    int g_j = 0;
+    bool g_page = false;
+    if (w < W_s) {
+        wave_units(U_s, W_s, w, s0, s1);
+        g_j = (int)((uint64_t)s0 / (uint32_t)units_s);
+        g_page = s0 - (int64_t)g_j * units_s < npu_s;
+    }
+    const int g_b = g_j / p.Hkv, g_kh = g_j - g_b * p.Hkv;
+    const int g_p0 = (int)(s0 - (int64_t)g_j * units_s);
+    const int g_p1 = (int)min((int64_t)npu_s, s1 - (int64_t)g_j * units_s);
+    SegSetup spec;
+    if (g_page)
+        spec = load_setup<GQ>(p, g_b, g_kh, g_p0, g_p1);
+    bool uniform = __ballot(lane < p.B && units_l != units_s) == 0;
+    for (int b0 = 64; b0 < p.B && uniform; b0 += 64) {
+        load_step(b0);
+        uniform = __ballot(b0 + lane < p.B && units_l != units_s) == 0;
+    }
+    int64_t U, u, u_last;
+    int W;
+    SeqUnits sq;
+    sq.fu = F;
+    if (uniform) {
+        if (w >= W_s)
+            return;
+        U = U_s;
+        W = W_s;
+        u = uniform64(s0);
+        u_last = uniform64(s1);
+        sq.b = g_b;
+        sq.base = (int64_t)g_b * p.Hkv * units_s;
+        sq.np_raw = p.B <= 64 ? __builtin_amdgcn_readlane(np_l, g_b) : p.num_pages[g_b];
+        sq.npu = seq_page_units(sq.np_raw, p.max_pages, F);
+    } else {
+        // ---- plan for U: prefix sums of the units, 64 sequences per step
+        if (p.B > 64)
+            load_step(0);  // the uniformity check moved on to later steps
+        int incl = wave_incl_scan(units_l, lane);
+        int64_t tot = __builtin_amdgcn_readlane(incl, 63);
+        for (int b0 = 64; b0 < p.B; b0 += 64) {
+            load_step(b0);
+            tot += __builtin_amdgcn_readlane(wave_incl_scan(units_l, lane), 63);
+        }
+        U = tot * p.Hkv;
+        W = plan_waves(U, p.page_waves, p.min_chunk);
+        if (w >= W)
+            return;
+        int64_t u_end;
+        wave_units(U, W, w, u, u_end);
+        u = uniform64(u);
+        u_last = uniform64(u_end);
+        // ---- the sequence holding unit u
+        int64_t base = 0;
+        for (int b0 = 0;; b0 += 64) {
+            if (b0 > 0) {
+                load_step(b0);
+                incl = wave_incl_scan(units_l, lane);
+            }
+            const unsigned long long hit = __ballot(b0 + lane < p.B && base + (int64_t)p.Hkv * incl > u);
+            if (hit || b0 + 64 >= p.B) {
+                const int lb = hit ? __builtin_ctzll(hit) : min(63, p.B - 1 - b0);  // second case not reached for u < U
+                sq.b = b0 + lb;
+                sq.base = base + (int64_t)p.Hkv * __builtin_amdgcn_readlane(incl - units_l, lb);
+                sq.np_raw = __builtin_amdgcn_readlane(np_l, lb);
+                sq.npu = seq_page_units(sq.np_raw, p.max_pages, F);
+                break;
+            }
+            base += (int64_t)p.Hkv * __builtin_amdgcn_readlane(incl, 63);
+        }
+    }
+    bool use_spec = uniform && g_page;  // the first segment is the one loaded above
+    int kh = uniform ? g_kh : (int)((uint32_t)(u - sq.base) / (uint32_t)(sq.npu + F));
+    const int Hkv = p.Hkv;
+#pragma clang loop unroll(disable)
+    for (;;) {
+        const int64_t u_end = u_last;
+        const int64_t per_pair = sq.npu + F;
+        const int64_t s_j = sq.base + kh * per_pair;
+        const int j = sq.b * Hkv + kh;
+        if (u == s_j && lane == 0)  // this wave starts the pair: its first partial
+            kernel_params(kp).ws_pair[2 * j] = w + 2 * j + (sq.npu > 0 ? 0 : 1);
+        const int64_t off = u - s_j;
+        if (off < sq.npu) {
+            const DecodeParams P = kernel_params(kp);
+            const int64_t e = min(u_end, s_j + sq.npu);
+            const int p0 = (int)off, p1 = (int)(e - s_j);
+            SegSetup su;
+            if (use_spec)
+                su = spec;
+            else
+                su = load_setup<GQ>(P, sq.b, kh, p0, p1);
+            use_spec = false;
+            page_segment<GQ>(P, stage0, stage1, sq.b, kh, sq.np_raw, p0, p1, (int64_t)w + 2 * j, su);
+            if (e == u_end && F > 0 && e == s_j + sq.npu)
+                empty_partial<GQ>(P, (int64_t)w + 2 * j + 1);
+            u = e;
+        } else {
+            use_spec = false;
+            const int64_t e = min(u_end, s_j + per_pair);
+            const int fa = (int)(off - sq.npu), fc = (int)(e - s_j - sq.npu);
+            const int ntok = seq_tokens(kernel_params(kp), sq.b);  // the tokens the F units share
+            fp16_partial<GQ>(kp, sq.b, kh, fa * ntok / F, fc * ntok / F, (int64_t)w + 2 * j + 1, stage0, stage1);
+            u = e;
+        }
+        if (u == s_j + per_pair && lane == 0)  // this wave ends the pair: its last partial
+            kernel_params(kp).ws_pair[2 * j + 1] = w + 2 * j + (F > 0 ? 1 : 0);
+        if (u >= u_end)
+            break;
+        if (u == s_j + per_pair && ++kh == Hkv) {
+            kh = 0;
+            const DecodeParams P = kernel_params(kp);
+            sq.b += 1;
+            sq.base += Hkv * per_pair;
+            sq.np_raw = P.num_pages[sq.b];
+            sq.npu = seq_page_units(sq.np_raw, P.max_pages, F);
+        }
+    }
+}
+
 static bool seg_aligned(const kitty_fp16_seg &s)
 {
     return ((uintptr_t)s.ptr & 15) == 0 && s.s_seq % 8 == 0 && s.s_head % 8 == 0 && s.s_tok % 8 == 0;
 }
 
+bool mfma_shape_supported(const DecodeParams &p)
+{
+    return p.D == 128 && p.G == 128 && p.Dk >= 0 && p.Dk <= 32 && (p.GQ == 4 || p.GQ == 8 || p.GQ == 16);
+}
+
 bool mfma_path_supported(const DecodeParams &p)
 {
-    return p.D == 128 && p.G == 128 && p.Dk >= 0 && p.Dk <= 32 && (p.GQ == 4 || p.GQ == 8 || p.GQ == 16) &&
+    return mfma_shape_supported(p) &&
            (p.flags & KITTY_DECODE_UNIQUE_BOOST_ROWS) && seg_aligned(p.sink_k) && seg_aligned(p.sink_v) &&
            seg_aligned(p.tail_k) && seg_aligned(p.tail_v) && ((uintptr_t)p.key_low & 15) == 0 &&
            ((uintptr_t)p.key_high & 15) == 0 && ((uintptr_t)p.key_meta & 15) == 0 &&
@@ -913,7 +1226,7 @@ bool mfma_path_supported(const DecodeParams &p)
 
 int launch_mfma(const DecodeParams &p, hipStream_t stream)
 {
-    dim3 grid(num_partials(p), p.Hkv, p.B);
+    dim3 grid((unsigned)p.page_waves);
     switch (p.GQ) {
     case 4: hipLaunchKernelGGL(decode_mfma_kernel<4>, grid, dim3(64), 0, stream, p); break;
     case 8: hipLaunchKernelGGL(decode_mfma_kernel<8>, grid, dim3(64), 0, stream, p); break;

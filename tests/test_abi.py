@@ -55,12 +55,22 @@ def test_invalid_arguments_are_rejected_without_launch():
 
 def test_workspace_size_formula():
     from kitty.kernels.ops import decode_workspace_bytes
-    # config 3 on 256 CUs (2048 resident waves): 128 pairs x 16 waves ->
-    # 15 splits of 17 pages + 1 FP16 split per pair
-    n = decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255)
-    assert n == 16 * 32 * 16 * (128 + 2) * 4
-    n = decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255, pages_per_split=200)  # capped at 64
-    assert n == 16 * 32 * (4 + 1) * (128 + 2) * 4
+    row = (128 + 2) * 4  # O + (m, l) per partial row, fp32
+    # Config 3 shape on 256 CUs.  Uniform plan (generic kernel): 15 splits of
+    # 17 pages + 1 FP16 split per (b, q head).  Unit-balanced plan (MFMA
+    # kernel): GQ rows per partial t < 2 (2048 resident waves + 128 pairs),
+    # plus the (first, last) partial table of the pairs.  The size covers both.
+    uniform = 16 * 32 * 16 * row
+    balanced = 2 * (2048 + 128) * 4 * row + 128 * 2 * 4
+    assert decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255) == max(uniform, balanced)
+    # pages_per_split = 200: uniform splits capped at 64 pages (4 + 1 per
+    # head); balanced: at least 200 units per wave, 128 pairs x ceil(256 / 200)
+    # waves
+    uniform = 16 * 32 * (4 + 1) * row
+    balanced = 2 * (128 * 2 + 128) * 4 * row + 128 * 2 * 4
+    assert decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255, pages_per_split=200) == max(uniform, balanced)
+    # a shape only the generic kernel takes (GQA 2): uniform plan alone
+    assert decode_workspace_bytes(16, 16, 8, 128, 128, 16, 255) == 16 * 16 * 16 * row
 
 
 def test_cpu_tensors_rejected_no_fallback():

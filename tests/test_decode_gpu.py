@@ -131,6 +131,19 @@ def test_batched_ragged_split_invariance(dev, pps):
         _close(out[b], _oracle_batched(c, Hq, H, D, b), f"b={b} pps={pps}")
 
 
+@pytest.mark.parametrize("Hq,pps", [(8, 16), (8, 6), (8, 3), (8, 2), (16, 3)])
+def test_merge_partial_counts(dev, Hq, pps):
+    """One long sequence cut into many partials per (sequence, KV head): at
+    least pps units per wave gives about 20, 52, 103 and 154 partials per pair
+    for pps 16, 6, 3 and 2 (306 units: 300 pages and 6 FP16 units), which takes
+    the merge through its one-pass paths for 32, 64 and 128 partials and its
+    two-pass path, for GQA groups of 4 and 8."""
+    B, H, D, G, dk = 1, 2, 128, 128, 16
+    c = _batched_case(dev, 50 + pps, B, Hq, H, D, G, dk, [32 + 300 * 128 + 50])
+    out = _run_batched(dev, c, pps)
+    _close(out[0], _oracle_batched(c, Hq, H, D, 0), f"Hq={Hq} pps={pps}")
+
+
 @pytest.mark.parametrize("name,B,Hq,H,ctx,dk", [
     ("config3", 16, 32, 8, 32768, 16),
     ("config5", 4, 64, 8, 131072, 16),
