@@ -41,9 +41,6 @@ static int fp16_weight(int GQ)
     return GQ <= 4 ? KITTY_FP16_WEIGHT_GQ4 : (GQ <= 8 ? KITTY_FP16_WEIGHT_GQ8 : KITTY_FP16_WEIGHT_GQ16);
 }
 constexpr int kMinChunk = 4;  // fewest units per wave of the unit-balanced plan
-#ifndef KITTY_PAGE_WAVES_16THS
-#define KITTY_PAGE_WAVES_16THS 16
-#endif
 
 // Split size.  Every (b, kh) pair gets n_splits page splits plus one FP16
 // split; when the batch allows it, the total is kept within one resident
@@ -88,7 +85,7 @@ static void set_plan(DecodeParams &p, const kitty_decode_args &a, bool balanced)
         p.page_waves = (int)(waves < 1 ? 1 : (waves > 16 * res ? 16 * res : waves));
     } else {
         p.min_chunk = kMinChunk;
-        p.page_waves = (int)(res * KITTY_PAGE_WAVES_16THS / 16);
+        p.page_waves = (int)res;  // every resident slot (fewer waves measured slower)
     }
 }
 
