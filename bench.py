@@ -259,18 +259,6 @@ def main() -> int:
     torch.cuda.synchronize()
 
     K = args.steps
-    # whole-job rate: K back-to-back decode steps between two HIP events
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record()
-    for i in range(K):
-        plans[i % len(plans)].run()
-    e1.record()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / K
-    step_us_events = e0.elapsed_time(e1) / K * 1e3
     # kernel durations: K back-to-back launches of the split kernel (the
     # dominant one), then K of the merge kernel, each burst between two HIP
     # events on the launch stream (an event pair per launch would add the
@@ -286,6 +274,19 @@ def main() -> int:
         return a.elapsed_time(b) / K * 1e3
     kernel_us = burst(lambda p: p.run_splits())
     merge_us = burst(lambda p: p.run_merge())
+    # whole-job rate, timed last (the GPU at its steady clock): K back-to-back
+    # decode steps between two HIP events
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(K):
+        plans[i % len(plans)].run()
+    e1.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / K
+    step_us_events = e0.elapsed_time(e1) / K * 1e3
     log(f"{ms_per_step * 1e3:.1f} us/step wall ({step_us_events:.1f} by events); "
         f"split kernel {kernel_us:.1f} us, merge {merge_us:.1f} us")
     achieved = nb["total"] / (kernel_us * 1e-6) / 1e9
