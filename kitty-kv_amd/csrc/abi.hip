@@ -42,11 +42,11 @@ static int fp16_weight(int GQ)
 }
 constexpr int kMinChunk = 4;  // fewest units per wave of the unit-balanced plan
 
-// Split size.  Every (b, kh) pair gets n_splits page splits plus one FP16
-// split; when the batch allows it, the total is kept within one resident
-// round of waves, because a handful of waves left over for a second round
-// doubles the kernel time.  Splits hold 4..kMaxPagesPerSplit pages (one page
-// id per lane of a wave).
+// Split size of the uniform plan (generic kernel).  Every (b, kh) pair gets
+// n_splits page splits plus one FP16 split; when the batch allows it, the
+// total is kept within one resident round of workgroups, because a handful
+// left over for a second round doubles the kernel time.  Splits hold
+// 4..kMaxPagesPerSplit pages.
 static int choose_pages_per_split(const kitty_decode_args &a, int n_fp16)
 {
     if (a.pages_per_split > 0)

@@ -1,9 +1,11 @@
 // MFMA split-K paged decode for the production shape (D = G = 128,
 // D_boost <= 32, GQA group 4, 8 or 16) on gfx950.
 //
-// One wave (64 lanes) owns a work item (sequence b, KV head kh, range of
-// pages).  Per page it streams the 9.5-10 KB (page, head) record from HBM
-// into registers one page ahead, parks it in a 10 KB LDS stage, and:
+// One wave (64 lanes) takes an equal share of the batch's work units (the
+// pages of every (sequence b, KV head kh) pair, then a weighted share of its
+// FP16 sink + tail tokens; see the unit-balanced plan in decode.h), one
+// segment per pair it touches.  Per page it streams the 9.5-10 KB
+// (page, head) record from HBM into a 10 KB LDS stage one page ahead, and:
 //
 //  QK   S[h][t] = sum_k A[h][k] * B[k][t] with v_mfma_f32_16x16x32_f16.
 //       B: 2-bit codes turned into fp16 by OR-ing them into the mantissa of
@@ -28,7 +30,7 @@
 //       treatment, so output tile a (channel slot a) accumulates 4^a O plus
 //       1024 sum_t P'; the per-token zero points and the 1024 offsets are
 //       subtracted from the accumulator at each page, and the 4^a is
-//       divided out when the split's partial is written.
+//       divided out when the segment's partial is written.
 //
 // Reduction index k of every MFMA follows the natural channel / token order
 // within a 32-wide step (the tr8 row order puts even and odd bytes of a
