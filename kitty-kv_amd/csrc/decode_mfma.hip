@@ -764,9 +764,15 @@ __device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned cha
     else if (p1 > np_raw)
         p1 = np_raw;
 
-    // rank -> channel map of this KV head (inverse of boost_idx), built in
-    // stage1 before any page lands there.
+    // rank -> channel map of this KV head (inverse of boost_idx) and the q
+    // rows of the group, staged in stage1 before any page lands there; the
+    // boosted channels' q values are then read from LDS, not by a global load
+    // that would wait on the map (one memory round trip before the first
+    // page's loads).
+    const bool head_row = (r % ROWS_PER_HEAD) == 0;
+    const int hr = r / ROWS_PER_HEAD;  // head of MFMA row r
     int *rank_chan = (int *)stage1;
+    _Float16 *q_lds = (_Float16 *)(stage1 + 256);  // [GQ][128]
     if (lane < 32)
         rank_chan[lane] = 0;
     __syncthreads();
@@ -774,16 +780,19 @@ __device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned cha
         rank_chan[su.bi0] = lane;
     if (su.bi1 < Dk)
         rank_chan[su.bi1] = 64 + lane;
+    if (GQ <= 8 && head_row) {  // (GQA 16 keeps the global loads: staged, its page loop waited on the prefetch)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            *(u32x4 *)(q_lds + hr * 128 + 32 * s + 8 * q) = su.qraw[s];
+    }
+
     __syncthreads();
 
     WaveState<GQ> W;
     W.cm = code_masks();
     // Static halves of the QK A operand: q * sm_scale * log2(e) / 2^e for the
     // lane's 8 channels of every K-step; zero on rows that carry no head.
-    const bool head_row = (r % ROWS_PER_HEAD) == 0;
-    const int hr = r / ROWS_PER_HEAD;  // head of MFMA row r
     W.prow = hr;
-    const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + hr) * p.q_s_head;
     const float qscale = head_row ? p.sm_scale * kLog2e : 0.0f;
     {
         const u32x4 *qraw = su.qraw;
@@ -791,9 +800,10 @@ __device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned cha
         for (int i = 0; i < 8; ++i)
             W.hch[i] = rank_chan[8 * q + i];
         _Float16 qh[8];
+        const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + hr) * p.q_s_head;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            qh[i] = *(const _Float16 *)(qrow + W.hch[i]);
+            qh[i] = GQ <= 8 ? q_lds[hr * 128 + W.hch[i]] : *(const _Float16 *)(qrow + W.hch[i]);
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -841,7 +851,7 @@ __device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned cha
 #pragma unroll
     for (int ch = 0; ch < 4; ++ch)
         W.o4[ch][0] = W.o4[ch][1] = 0.0f;
-    __syncthreads();  // rank_chan reads done before stage1 is overwritten
+    __syncthreads();  // stage1 reads done before the next page lands there
 
     // Page ids, 64 at a time (one per lane), read back with v_readlane so no
     // page waits on a dependent global load; pages are asked for in order,
