@@ -1149,10 +1149,11 @@ void decode_mfma_kernel(DecodeParams p)
         wave_units(U, W, w, u, u_end);
         u = uniform64(u);
         u_last = uniform64(u_end);
-        // ---- the sequence holding unit u
+        // ---- the sequence holding unit u (with more than 64 sequences the
+        // total above moved the step registers on: start again from step 0)
         int64_t base = 0;
         for (int b0 = 0;; b0 += 64) {
-            if (b0 > 0) {
+            if (b0 > 0 || p.B > 64) {
                 load_step(b0);
                 incl = wave_incl_scan(units_l, lane);
             }
@@ -1171,6 +1172,8 @@ void decode_mfma_kernel(DecodeParams p)
     bool use_spec = uniform && g_page;  // the first segment is the one loaded above
     int kh = uniform ? g_kh : (int)((uint32_t)(u - sq.base) / (uint32_t)(sq.npu + F));
     const int Hkv = p.Hkv;
+    if (sq.b < 0 || sq.b >= p.B || kh < 0 || kh >= Hkv || u < sq.base)
+        return;  // not reached: the plan places every unit in a pair of the batch
 #pragma clang loop unroll(disable)
     for (;;) {
         const int64_t u_end = u_last;

@@ -144,6 +144,40 @@ def test_merge_partial_counts(dev, Hq, pps):
     _close(out[0], _oracle_batched(c, Hq, H, D, 0), f"Hq={Hq} pps={pps}")
 
 
+@pytest.mark.parametrize("case", ["gqa16", "b70_uniform", "b70_ragged", "no_boost", "page_count_poison"])
+def test_mfma_plan_edge_cases(dev, case):
+    """Shapes the MFMA kernel's work plan treats specially, against the
+    oracle: GQA 16 (one wave per SIMD, its own q set-up), more than 64
+    sequences (the plan scans the batch 64 sequences at a time; uniform and
+    ragged), no boosted channels, and a page count above max_pages (that
+    sequence's output is NaN, the others are unaffected)."""
+    D, G = 128, 128
+    if case == "gqa16":
+        B, Hq, H, dk = 3, 32, 2, 16
+        ctx = [32 + 5 * 128 + 10, 32 + 40 * 128 + 100, 32]
+    elif case == "b70_uniform":
+        B, Hq, H, dk = 70, 8, 2, 16
+        ctx = [32 + 3 * 128 + 20] * B
+    elif case == "b70_ragged":
+        B, Hq, H, dk = 70, 8, 2, 16
+        ctx = [int(x) for x in ragged_lengths(7, B, 32, 32 + 12 * 128)]
+    elif case == "no_boost":
+        B, Hq, H, dk = 2, 16, 2, 0
+        ctx = [32 + 9 * 128 + 7, 32 + 2 * 128 + 127]
+    else:
+        B, Hq, H, dk = 3, 8, 2, 16
+        ctx = [32 + 4 * 128 + 3, 32 + 4 * 128 + 3, 32 + 2 * 128]
+    c = _batched_case(dev, 60 + len(case), B, Hq, H, D, G, dk, ctx)
+    if case == "page_count_poison":
+        c["n_pages"][1] = c["bt"].shape[1] + 1   # above max_pages (the table width)
+    out = _run_batched(dev, c)
+    for b in range(B):
+        if case == "page_count_poison" and b == 1:
+            assert np.isnan(out[b]).all()
+            continue
+        _close(out[b], _oracle_batched(c, Hq, H, D, b), f"{case} b={b}")
+
+
 @pytest.mark.parametrize("name,B,Hq,H,ctx,dk", [
     ("config3", 16, 32, 8, 32768, 16),
     ("config5", 4, 64, 8, 131072, 16),
