@@ -17,9 +17,14 @@
 // packed rows, the page is assembled in LDS, and the workgroup writes the
 // 4 KB code region with one 16-byte store per thread.
 //
+// The block's loads do not wait for anything: rows past the valid ones read
+// a zero row instead of branching, and the destination page id is looked up
+// after the loads are issued.
+//
 // Arithmetic is that of quantize.h (bit-exact with the reference); the codes
 // use the multiply-by-reciprocal of rint_quot below, which returns the same
-// integer as rint of the correctly rounded quotient.
+// integer as rint of the correctly rounded quotient, checked eight elements
+// at a time (rint_quot8).
 #include "quantize.h"
 
 #pragma clang fp contract(off)
@@ -76,19 +81,50 @@ __device__ __forceinline__ float rint_quot(float x, float s, float rs)
     return n;
 }
 
+// rint_quot of eight elements that share (s, rs), with one branch for the
+// eight: when any of them lies near a half-integer, all eight are recomputed
+// from the correctly rounded quotient (which the fast path only reproduces).
+__device__ __forceinline__ void rint_quot8(const float (&x)[8], float s, float rs, float (&n)[8])
+{
+    float dev = 0.0f;  // largest |y - rint(y)| of the eight
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float y = x[e] * rs;
+        n[e] = __builtin_rintf(y);
+        dev = __builtin_fmaxf(dev, __builtin_fabsf(y - n[e]));
+    }
+    if (__builtin_expect(dev > 0.5f - 0x1p-14f, 0)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            n[e] = __builtin_rintf(x[e] / s);
+    }
+}
+
 // clamp(n + z, 0, mq) -> code; n and z are small integers, so v_med3 is exact.
 __device__ __forceinline__ unsigned code_of(float n, float z, float mq)
 {
     return (unsigned)__builtin_amdgcn_fmed3f(n + z, 0.0f, mq);
 }
 
-// Rows t0..t0+7 of a token-major fp16 block, 8 channels each; rows at or past
-// `rows_valid` read as zeros (the reference's zero-padded value rows).
-__device__ __forceinline__ void load_rows(const uint16_t *src, int64_t s_tok, int t0, int rows_valid, u32x4 (&r)[8])
+// 256 bytes of zeros: the rows of a block past `rows_valid` are loaded from
+// here (16 bytes per lane of a token row; never written).
+__device__ u32x4 kZeroRow[16];
+
+// Rows t0..t0+7 of a token-major fp16 block, channels 8cg..8cg+7 (`src`
+// already points at channel 8cg); rows at or past `rows_valid` read as zeros
+// (the reference's zero-padded value rows).  Every load is issued
+// unconditionally, the eight together: a row past the block reads the zero
+// row instead, so no branch (and no wait at its join) separates the loads.
+// The source is read once: the loads are non-temporal.
+__device__ __forceinline__ void load_rows(const uint16_t *src, int64_t s_tok, int t0, int rows_valid, int cg,
+                                          u32x4 (&r)[8])
 {
+    const uint16_t *base = src + (int64_t)t0 * s_tok;
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-        r[k] = (t0 + k < rows_valid) ? *(const u32x4 *)(src + (int64_t)(t0 + k) * s_tok) : u32x4{0u, 0u, 0u, 0u};
+    for (int k = 0; k < 8; ++k) {
+        const u32x4 *ptr = t0 + k < rows_valid ? (const u32x4 *)(base + k * s_tok) : &kZeroRow[cg];
+        r[k] = __builtin_nontemporal_load(ptr);
+    }
 }
 
 // Code region of the page (128 rows x 32 B, contiguous): one 16-byte store per thread.
@@ -112,9 +148,19 @@ __device__ __forceinline__ void read8(const unsigned char *lds, int off, T (&v)[
     }
 }
 
+// Destination page of block (o, i), looked up after the block's loads are
+// issued so that they do not wait for it.  A page id outside the pool, or a
+// head past the pool's heads, writes nothing (never outside the pools).
+__device__ __forceinline__ int64_t dest_page(const QuantLaunch &L, int o, int i, bool &ok)
+{
+    const int64_t page = L.qb.page_ids[o];
+    ok = page >= 0 && page < L.st.num_pages && i < L.st.num_kv_heads;
+    return page;
+}
+
 // ------------------------------------------------------------------- keys
 // quantize_key.py:69-124: per channel over the 128 tokens.
-__device__ void key_block(const QuantLaunch &L, int o, int i, int64_t page, unsigned char *lds)
+__device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds)
 {
     const kitty_page_store &st = L.st;
     const kitty_quant_batch &qb = L.qb;
@@ -123,8 +169,11 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, int64_t page, unsi
     const int Dk = st.d_boost;
 
     u32x4 r[8];
-    load_rows(qb.key + o * qb.key_s_outer + i * qb.key_s_inner + 8 * cg, qb.key_s_tok, 8 * tt, 128, r);
-    const int b = tid < 128 ? qb.boost_idx[o * qb.boost_s_outer + i * qb.boost_s_inner + tid] : 0;
+    load_rows(qb.key + o * qb.key_s_outer + i * qb.key_s_inner + 8 * cg, qb.key_s_tok, 8 * tt, 128, cg, r);
+    // boost rank of channel tid (threads 128.. load a copy and ignore it)
+    const int b = qb.boost_idx[o * qb.boost_s_outer + i * qb.boost_s_inner + (tid & 127)];
+    bool ok;
+    const int64_t page = dest_page(L, o, i, ok);
 
     unsigned *high = (unsigned *)(lds + kHighOff);
     for (int e = tid; e < Dk * 8; e += kThreads)
@@ -175,9 +224,11 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, int64_t page, unsi
         pz[tid] = z;
         pmq[tid] = mq;
         phr[tid] = b < Dk ? b : -1;                                    // :113-116
-        const int64_t m = page * st.key_meta_s_page + i * st.key_meta_s_head + tid;
-        st.key_scale[m] = f2h(s);                                      // :121-122
-        st.key_zero[m] = f2h(z);
+        if (ok) {
+            const int64_t m = page * st.key_meta_s_page + i * st.key_meta_s_head + tid;
+            st.key_scale[m] = f2h(s);                                  // :121-122
+            st.key_zero[m] = f2h(z);
+        }
     }
     __syncthreads();
 
@@ -190,10 +241,15 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, int64_t page, unsi
     read8(lds, kParOff + 2048 + 32 * cg, hr);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
+        float x[8], n[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            x[k] = chan(r[k], c);
+        rint_quot8(x, s[c], rs[c], n);
         unsigned lo = 0, hi = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {                                  // :95-103
-            const unsigned q = code_of(rint_quot(chan(r[k], c), s[c], rs[c]), z[c], mq[c]);
+            const unsigned q = code_of(n[k], z[c], mq[c]);
             lo |= (q & 3u) << (2 * k);
             hi |= ((q >> 2) & 3u) << (2 * k);
         }
@@ -203,6 +259,8 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, int64_t page, unsi
             atomicOr(high + hr[c] * 8 + (tt >> 1), hi << (16 * (tt & 1)));
     }
     __syncthreads();
+    if (!ok)
+        return;
     store_tile(st.key_low + page * st.key_low_s_page + i * st.key_low_s_head, lds, tid);
     if (tid < 2 * Dk)
         *(u32x4 *)(st.key_high + page * st.key_high_s_page + i * st.key_high_s_head + 16 * tid) =
@@ -211,7 +269,7 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, int64_t page, unsi
 
 // ----------------------------------------------------------------- values
 // quantize_value.py:58-90: per token over the 128 channels.
-__device__ void value_block(const QuantLaunch &L, int o, int i, int64_t page, unsigned char *lds)
+__device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *lds)
 {
     const kitty_page_store &st = L.st;
     const kitty_quant_batch &qb = L.qb;
@@ -220,7 +278,9 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, int64_t page, un
 
     u32x4 r[8];
     load_rows(qb.value + o * qb.value_s_outer + i * qb.value_s_inner + 8 * cg, qb.value_s_tok, 8 * tt,
-              qb.value_rows, r);
+              qb.value_rows, cg, r);
+    bool ok;
+    const int64_t page = dest_page(L, o, i, ok);
 
     // (min, -max) of each token over the thread's 8 channels, packed in fp16,
     // then over the 16 lanes of the DPP row (:63-64)
@@ -255,7 +315,8 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, int64_t page, un
         prs[t] = rs;
         pz[t] = z;
         const int64_t m = page * st.value_meta_s_page + i * st.value_meta_s_head + 2 * t;
-        *(unsigned *)(st.value_scale + m) = (unsigned)f2h(s) | ((unsigned)f2h(z) << 16);  // :90, interleaved
+        if (ok)
+            *(unsigned *)(st.value_scale + m) = (unsigned)f2h(s) | ((unsigned)f2h(z) << 16);  // :90, interleaved
     }
     __syncthreads();
 
@@ -265,14 +326,20 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, int64_t page, un
     read8(lds, kParOff + 1024 + 32 * tt, z);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
+        float x[8], n[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            x[c] = chan(r[k], c);
+        rint_quot8(x, s[k], rs[k], n);
         unsigned bits = 0;
 #pragma unroll
         for (int c = 0; c < 8; ++c)                                    // :74-88, channel 4j+i at byte j bits 2i
-            bits |= code_of(rint_quot(chan(r[k], c), s[k], rs[k]), z[k], 3.0f) << (2 * c);
+            bits |= code_of(n[c], z[k], 3.0f) << (2 * c);
         *(uint16_t *)(lds + tile_off(8 * tt + k) + 2 * cg) = (uint16_t)bits;
     }
     __syncthreads();
-    store_tile(st.value + page * st.value_s_page + i * st.value_s_head, lds, tid);
+    if (ok)
+        store_tile(st.value + page * st.value_s_page + i * st.value_s_head, lds, tid);
 }
 
 __global__ __launch_bounds__(kThreads) void quantize_page128_kernel(QuantLaunch L)
@@ -280,14 +347,11 @@ __global__ __launch_bounds__(kThreads) void quantize_page128_kernel(QuantLaunch 
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
     const int n = blockIdx.x;
     const int o = n / L.qb.n_inner, i = n - o * L.qb.n_inner;
-    const int64_t page = L.qb.page_ids[o];
-    if (page < 0 || page >= L.st.num_pages || i >= L.st.num_kv_heads)
-        return; // never write outside the pools
     if (blockIdx.y == 0) {
         if (L.qb.key)
-            key_block(L, o, i, page, lds);
+            key_block(L, o, i, lds);
     } else if (L.qb.value) {
-        value_block(L, o, i, page, lds);
+        value_block(L, o, i, lds);
     }
 }
 
