@@ -22,6 +22,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -166,8 +167,8 @@ def bench_quantize(torch, dev, reps: int = 64) -> dict:
     """4096 tokens x 8 KV heads x 128, batch quantize + pack.
     Sixteen input / output sets (309 MB, more than the 256 MB MALL) rotate;
     `reps` launches are enqueued back to back between two HIP events
-    (pre-built arguments, so the GPU never waits for the host) and the mean per
-    launch is reported."""
+    (pre-built arguments, so the GPU never waits for the host); the mean per
+    launch of the median of five such bursts is reported."""
     from kitty.kernels.ops import QuantizePlan, pool_store
     T, H, dk, sets = 4096, 8, 16, 16
     n = T // G
@@ -193,13 +194,16 @@ def bench_quantize(torch, dev, reps: int = 64) -> dict:
     for p in plans:
         p.run()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(reps):
-        plans[i % sets].run()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) / reps * 1e3
+
+    def burst() -> float:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(reps):
+            plans[i % sets].run()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+    us = statistics.median(burst() for _ in range(5))
     read = 2 * T * H * D * 2
     written = n * H * (D * G // 4 + dk * G // 4 + 2 * D * 2 + G * D // 4 + G * 2 * 2)
     return {"workload": "cfg2: 4096 tok x 8 KV heads x 128, 12.5% INT4", "us": round(us, 2),
@@ -259,10 +263,12 @@ def main() -> int:
     torch.cuda.synchronize()
 
     K = args.steps
-    # kernel durations: K back-to-back launches of the split kernel (the
-    # dominant one), then K of the merge kernel, each burst between two HIP
+    # kernel durations: bursts of K back-to-back launches of the split kernel
+    # (the dominant one), then of the merge kernel, each burst between two HIP
     # events on the launch stream (an event pair per launch would add the
-    # dispatch latency of every launch to the kernel time)
+    # dispatch latency of every launch to the kernel time).  The median of
+    # five bursts: the first one after start-up can run while the GPU clock
+    # is still rising.
     def burst(fn) -> float:
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
@@ -272,8 +278,8 @@ def main() -> int:
         b.record()
         torch.cuda.synchronize()
         return a.elapsed_time(b) / K * 1e3
-    kernel_us = burst(lambda p: p.run_splits())
-    merge_us = burst(lambda p: p.run_merge())
+    kernel_us = statistics.median(burst(lambda p: p.run_splits()) for _ in range(5))
+    merge_us = statistics.median(burst(lambda p: p.run_merge()) for _ in range(5))
     # whole-job rate, timed last (the GPU at its steady clock): K back-to-back
     # decode steps between two HIP events
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
