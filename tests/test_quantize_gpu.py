@@ -143,20 +143,22 @@ def test_rounding_boundaries_bit_exact(dev):
         _check_page(pools, 1, h, K[h].T.copy(), V[h], bi[h].numpy(), Dk, Dk + 1)
 
 
-def test_value_rows_zero_padding(dev):
-    """Rows past value_rows quantise as zeros (pipeline.py:240-243)."""
+@pytest.mark.parametrize("rows", [0, 1, 37, 127])
+def test_value_rows_zero_padding(dev, rows):
+    """Rows past value_rows quantise as zeros (pipeline.py:240-243); the
+    128 x 128 kernel reads them from a zero row, not from the source."""
     from kitty.kernels.ops import quantize_into_pools
     D, G, H = 128, 128, 2
-    gen = torch.Generator().manual_seed(11)
+    gen = torch.Generator().manual_seed(11 + rows)
     V = torch.randn(1, H, G, D, generator=gen).half()
     pools, store = _pools(1, H, D, G, 16, dev)
     quantize_into_pools(store, None, V.to(dev), None, torch.zeros(1, dtype=torch.int32, device=dev), 17,
-                        value_rows=37)
+                        value_rows=rows)
     torch.cuda.synchronize()
     vp, vm = pools[3].cpu().numpy(), pools[4].cpu().numpy()
     for h in range(H):
         v = V[0, h].numpy().copy()
-        v[37:] = 0
+        v[rows:] = 0
         pk, sv, zv = O.quantize_value(v)
         assert np.array_equal(vp[0, h], pk) and _eq16(vm[0, h, :, 0], sv) and _eq16(vm[0, h, :, 1], zv)
 
