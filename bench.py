@@ -157,13 +157,48 @@ def cpu_baseline(w, budget_s: float) -> dict:
     # scale by pages: the oracle's time is linear in the pages it walks
     total_pages = sum(w["np_list"])
     value = t_total * total_pages / max(pages_done, 1)
-    return {"value": round(value * 1e6, 1), "unit": "us/layer-step", "cores": 1, "kind": "port",
+    return {"value": round(value * 1e6, 1), "unit": "us/layer-step", "cores": 1, "kind": "port", **host_cpu(),
             "sample": f"{done} of {w['B']} sequences ({pages_done} of {total_pages} pages, all {w['Hkv']} KV heads, "
                       f"{S} sinks + FP16 tail each) through oracle/kitty_oracle.c (paged_attention_reference "
                       f"restated), single thread; scaled by pages to one layer-step"}
 
 
-def bench_quantize(torch, dev, reps: int = 64) -> dict:
+def host_cpu() -> dict:
+    """Host CPU of this run: model string and the threads the OS offers."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "host_threads": os.cpu_count()}
+
+
+def quantize_cpu_baseline(k, v, bi, dk: int) -> dict:
+    """Oracle C port of quantize_key_page_torch / quantize_value_page_torch,
+    one thread, over every block of one config-2 batch (256 key + 256 value
+    blocks; a few hundred ms)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    O.build()
+    kc, vc, bic = k.cpu().numpy(), v.cpu().numpy(), bi.cpu().numpy()   # (T, H, D), (H, D)
+    T, H, _ = kc.shape
+    t0 = time.perf_counter()
+    for p0 in range(0, T, G):
+        for h in range(H):
+            O.quantize_key(kc[p0:p0 + G, h].T, bic[h], dk, dk + 1)     # the reference quantises (D, G) keys
+            O.quantize_value(vc[p0:p0 + G, h])
+    us = (time.perf_counter() - t0) * 1e6
+    return {"value": round(us, 1), "unit": "us/batch", "cores": 1, "kind": "port", **host_cpu(),
+            "sample": f"all {T // G * H} key + {T // G * H} value blocks of one config-2 batch through "
+                      f"oracle/kitty_oracle.c (quantize_key_page_torch / quantize_value_page_torch restated), "
+                      f"single thread"}
+
+
+def bench_quantize(torch, dev, reps: int = 64, cpu: bool = False) -> dict:
     """4096 tokens x 8 KV heads x 128, batch quantize + pack.
     Sixteen input / output sets (309 MB, more than the 256 MB MALL) rotate;
     `reps` launches are enqueued back to back between two HIP events
@@ -181,14 +216,19 @@ def bench_quantize(torch, dev, reps: int = 64) -> dict:
     store = pool_store(*pools)
     gcpu = torch.Generator().manual_seed(2)
     bi = torch.full((H, D), dk + 1, dtype=torch.uint8)
+    scale = torch.ones(H, D)
     for h in range(H):
-        bi[h, torch.randperm(D, generator=gcpu)[:dk]] = torch.arange(dk, dtype=torch.uint8)
-    bi = bi.to(dev)
+        ch = torch.randperm(D, generator=gcpu)[:dk]   # the head's outlier channels, quantised to INT4
+        bi[h, ch] = torch.arange(dk, dtype=torch.uint8)
+        scale[h, ch] = 8.0
+    bi, scale = bi.to(dev), scale.to(dev)
     plans = []
     for i in range(sets):
-        k = torch.randn(T, H, D, device=dev, generator=g).half()
+        k = (torch.randn(T, H, D, device=dev, generator=g) * scale).half()
         v = torch.randn(T, H, D, device=dev, generator=g).half()
         pids = torch.arange(i * n, (i + 1) * n, dtype=torch.int32, device=dev)
+        if i == 0:
+            k0, v0 = k, v
         plans.append(QuantizePlan(store, k.view(n, G, H, D).permute(0, 2, 1, 3),
                                   v.view(n, G, H, D).permute(0, 2, 1, 3), bi, pids, dk + 1))
     for p in plans:
@@ -204,11 +244,16 @@ def bench_quantize(torch, dev, reps: int = 64) -> dict:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps * 1e3
     us = statistics.median(burst() for _ in range(5))
+    cpu_base = quantize_cpu_baseline(k0, v0, bi, dk) if cpu else None
     read = 2 * T * H * D * 2
     written = n * H * (D * G // 4 + dk * G // 4 + 2 * D * 2 + G * D // 4 + G * 2 * 2)
-    return {"workload": "cfg2: 4096 tok x 8 KV heads x 128, 12.5% INT4", "us": round(us, 2),
-            "GBps": round((read + written) / us / 1e3, 1), "frac": round((read + written) / us / 1e3 / HBM_PEAK_GBPS, 4),
-            "bytes_read": read, "bytes_written": written}
+    out = {"workload": "cfg2: 4096 tok x 8 KV heads x 128, 16 x8 outlier key channels per head as INT4",
+           "us": round(us, 2),
+           "GBps": round((read + written) / us / 1e3, 1), "frac": round((read + written) / us / 1e3 / HBM_PEAK_GBPS, 4),
+           "bytes_read": read, "bytes_written": written}
+    if cpu_base:
+        out["cpu_baseline"] = cpu_base
+    return out
 
 
 def copy_probe(torch, dev) -> int:
@@ -335,7 +380,7 @@ def main() -> int:
                      "packed_kv_frac": round(packed_gbps / HBM_PEAK_GBPS, 4)},
     }
     if not args.no_quantize:
-        result["quantize_pack"] = bench_quantize(torch, dev)
+        result["quantize_pack"] = bench_quantize(torch, dev, cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         log("timing CPU baseline (oracle port, 1 thread)")
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
