@@ -70,13 +70,16 @@ def test_tail_length_mismatch_raises(dev):
         paged_attention(q, [int(c["pages"][0])], kb, kh, km, vp, vm, bi, 4, sk, sv, tk, tv[:, :3], 2, 2, 16)
 
 
-def _batched_case(dev, seed, B, Hq, H, D, G, dk, ctx, S=32, shuffle=True, pool_extra=7):
-    """Random-encoding pools, ctx[b] tokens per sequence = S sinks + pages + tail."""
+def _batched_case(dev, seed, B, Hq, H, D, G, dk, ctx, S=32, shuffle=True, pool_extra=7, bi_edit=None):
+    """Random-encoding pools, ctx[b] tokens per sequence = S sinks + pages + tail.
+    bi_edit(bi) may rewrite the boost ranks before the pools are drawn."""
     gen = torch.Generator().manual_seed(seed)
     sentinel = dk + 1
     bi = torch.full((H, D), sentinel, dtype=torch.uint8)
     for h in range(H):
         bi[h, torch.randperm(D, generator=gen)[:dk]] = torch.arange(dk, dtype=torch.uint8)
+    if bi_edit is not None:
+        bi_edit(bi)
     n_pages = [(c - S) // G for c in ctx]
     tails = [(c - S) % G for c in ctx]
     P = sum(n_pages) + pool_extra
@@ -190,6 +193,26 @@ def test_full_size_configs(dev, name, B, Hq, H, ctx, dk):
     out = _run_batched(dev, c)
     for b in range(B):
         _close(out[b], _oracle_batched(c, Hq, H, D, b), f"{name} b={b}")
+
+
+def test_duplicate_boost_ranks_take_the_generic_path(dev):
+    """Channels sharing a boost rank read the same high-bit row back
+    (dequantize_key.py:70-87) and a channel ranked D_boost has none: the MFMA
+    kernel assumes one channel per rank, so the batched decode detects the
+    repeated rank and runs the generic kernel, which matches the oracle."""
+    from kitty.kernels.ops import boost_rows_unique
+
+    def edit(bi):
+        r0, r1 = (bi[0] == 0).nonzero()[0, 0], (bi[0] == 1).nonzero()[0, 0]
+        assert r0 != r1
+        bi[0, r1] = 0                                    # rank 0 twice in head 0
+        bi[3, (bi[3] == 17).nonzero()[0, 0]] = 16        # head 3: one channel ranked D_boost
+    c = _batched_case(dev, 41, 3, 32, 8, 128, 128, 16, [32 + 128 * 5 + 17, 32 + 128 * 3, 32 + 128 * 9 + 100],
+                      bi_edit=edit)
+    assert not boost_rows_unique(c["bi"], 16)
+    out = _run_batched(dev, c)
+    for b in range(3):
+        _close(out[b], _oracle_batched(c, 32, 8, 128, b), f"dup b={b}")
 
 
 def test_invalid_page_id_poisons_output(dev):

@@ -102,6 +102,30 @@ def test_small_shapes_and_edge_rows(dev, D, G, Dk, H):
                         Dk, sentinel)
 
 
+def test_duplicate_and_rowless_boost_ranks(dev):
+    """Channels sharing a boost rank OR their high bits into the rank's row,
+    and a channel ranked D_boost (below the sentinel) gets INT4 codes with no
+    high row (quantize_key.py:73, 113-119); 128 x 128 kernel, bit-exact."""
+    from kitty.kernels.ops import quantize_into_pools
+    D = G = 128
+    H, Dk, sentinel = 2, 16, 17
+    gen = torch.Generator().manual_seed(77)
+    K = torch.randn(1, H, G, D, generator=gen).half()
+    bi = torch.full((1, H, D), sentinel, dtype=torch.uint8)
+    for h in range(H):
+        ch = torch.randperm(D, generator=gen)[:Dk + 1]
+        bi[0, h, ch[:Dk]] = torch.arange(Dk, dtype=torch.uint8)
+        bi[0, h, ch[1]] = 0      # rank 0 three times, ranks 1 and 2 unused (their rows stay 0)
+        bi[0, h, ch[2]] = 0
+        bi[0, h, ch[Dk]] = Dk    # INT4 codes, high bits not stored
+    pools, store = _pools(1, H, D, G, Dk, dev)
+    quantize_into_pools(store, K.to(dev), None, bi.to(dev), torch.zeros(1, dtype=torch.int32, device=dev),
+                        sentinel)
+    torch.cuda.synchronize()
+    for h in range(H):
+        _check_page(pools, 0, h, K[0, h].numpy().T.copy(), None, bi[0, h].numpy(), Dk, sentinel)
+
+
 def _boundary_block(gen, G, D, mq_of_col):
     """fp16 values at and one fp16 ulp either side of the rounding boundaries
     (j + 1/2) * s of rint(x / s), for exact (s = 1) and inexact (s = 1/3,
