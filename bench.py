@@ -150,6 +150,14 @@ def cpu_baseline(w, budget_s: float) -> dict:
                 w["dk"], w["sk"][b].cpu().numpy(), w["sv"][b].cpu().numpy(), w["tk"][b, :, :n].cpu().numpy(),
                 w["tv"][b, :, :n].cpu().numpy(), w["Hq"], w["Hkv"], D)
         t0 = time.perf_counter()
+        # the reference's first pass over the pages (attention.py:100-132)
+        # dequantises every (page, head) and discards the result
+        skb, skh, skm, svp, svm = sub
+        bin_ = args[7]
+        for pg in range(npb):
+            for h in range(w["Hkv"]):
+                O.dequantize_key(skb[pg, h], skh[pg, h], skm[pg, h, 0], skm[pg, h, 1], bin_[h], w["dk"])
+                O.dequantize_value(svp[pg, h], svm[pg, h, :, 0], svm[pg, h, :, 1])
         O.paged_attention(*args, n_threads=1)
         t_total += time.perf_counter() - t0
         done += 1
@@ -160,7 +168,8 @@ def cpu_baseline(w, budget_s: float) -> dict:
     return {"value": round(value * 1e6, 1), "unit": "us/layer-step", "cores": 1, "kind": "port", **host_cpu(),
             "sample": f"{done} of {w['B']} sequences ({pages_done} of {total_pages} pages, all {w['Hkv']} KV heads, "
                       f"{S} sinks + FP16 tail each) through oracle/kitty_oracle.c (paged_attention_reference "
-                      f"restated), single thread; scaled by pages to one layer-step"}
+                      f"restated, with its discarded first dequantisation pass), single thread; scaled by pages "
+                      f"to one layer-step"}
 
 
 def host_cpu() -> dict:
