@@ -83,6 +83,16 @@ __host__ __device__ inline int plan_waves(int64_t U, int page_waves, int min_chu
     return w < 1 ? 1 : w;
 }
 
+// Workgroup i of a launch runs on XCD i % 8 (each XCD has its own L2).  When
+// n % 8 == 0, logical index xcd_local_index(i, n) puts n / 8 consecutive
+// indices on each XCD, so work that shares data (the waves of one (b, kh)
+// pair, whose partials the merge of that pair reads back) shares an L2.
+constexpr int kXcds = 8;
+__host__ __device__ inline int xcd_local_index(int i, int n)
+{
+    return n % kXcds == 0 ? (i % kXcds) * (n / kXcds) + i / kXcds : i;
+}
+
 size_t generic_lds_bytes(int GQ, int D, int G, int Dk);
 int launch_generic(const DecodeParams &p, hipStream_t stream);
 int launch_splits(const DecodeParams &p, hipStream_t stream);

@@ -337,7 +337,9 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
     constexpr int kBatch = 32;
     constexpr int kOnePass = 128;  // partials merged in one round trip (two per lane)
     const int lane = threadIdx.x;
-    const int bq = blockIdx.x;
+    // (b, qh) on the XCD whose split waves wrote the pair's partials (for a
+    // uniform batch whose pair count is a multiple of 8)
+    const int bq = xcd_local_index(blockIdx.x, gridDim.x);
     const int b = bq / p.Hq, qh = bq - b * p.Hq;
     // Partials of this query head: NS rows from row0, step rstep apart
     // (uniform plan: consecutive rows; unit-balanced plan: partials t_first ..

@@ -1080,7 +1080,7 @@ void decode_mfma_kernel(DecodeParams p)
 
     const int lane = threadIdx.x;
     const KernargParams kp = (KernargParams)__builtin_amdgcn_kernarg_segment_ptr();
-    const int w = blockIdx.x;
+    const int w = xcd_local_index(blockIdx.x, gridDim.x);
     const int F = p.fp16_units;
     // ---- the plan's input, page counts 64 sequences per step (issued first)
     int np_l = 0, units_l = 0;  // sequence b0 + lane of the current step
