@@ -1068,7 +1068,8 @@ __device__ __forceinline__ void fp16_partial(KernargParams kp, int b, int kh, in
 //
 // Wave w works through units [w U / W, (w + 1) U / W) of the unit-balanced
 // plan: a run of pages or of FP16 tokens of one pair per segment, one
-// partial per segment.
+// partial per segment.  w is the workgroup's XCD-local order
+// (xcd_local_index), so the consecutive waves of a pair share an XCD and its L2.
 template <int GQ>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(GQ <= 8 ? 2 : 1)))
 void decode_mfma_kernel(DecodeParams p)
