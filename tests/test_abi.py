@@ -85,3 +85,14 @@ def test_cpu_tensors_rejected_no_fallback():
                         torch.zeros(1, 16, dtype=torch.uint8), 0, torch.zeros(1, 0, 16).half(),
                         torch.zeros(1, 0, 16).half(), torch.zeros(1, 0, 16).half(), torch.zeros(1, 0, 16).half(),
                         1, 1, 16)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with a message (status 2)
+    before touching a device."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
