@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KITTY_ABI_VERSION 1
+#define KITTY_ABI_VERSION 2
 
 #define KITTY_OK 0
 #define KITTY_E_INVALID (-1)     /* bad shape, stride, alignment or null pointer */
@@ -129,14 +129,23 @@ int kitty_dequantize_value_page(const kitty_page_store *store, int64_t page, int
  * (kitty/kernels/attention.py:46-189, 292-341), batched over B sequences.
  *
  * For sequence b and query head qh (KV head kh = qh / (Hq/Hkv), :177) the
- * attended tokens are, in order:
- *   sink_len[b] FP16 sinks, num_pages[b] quantised pages
- *   (block_table[b*bt_stride + p], p < num_pages[b]), tail_len[b] FP16 tail
- *   tokens (key tail = KittyInferencePipeline.key_qbuf, value tail =
- *   val_local; the reference appends the tail only when it is non-empty and
- *   requires equal key / value tail lengths, :163-165).
+ * key and value streams are
+ *   K: sink_len[b] FP16 sinks | key pages p < num_pages[b]
+ *      (block_table[b*bt_stride + p]) | tail_len[b] FP16 key-tail tokens
+ *   V: sink_len[b] FP16 sinks | value pages p < num_pages_v[b] (same block
+ *      table entries) | tail_len_v[b] FP16 value-tail tokens
+ * and cover the same tokens: num_pages_v[b] <= num_pages[b] and
+ * (num_pages[b] - num_pages_v[b]) * page_tokens + tail_len[b] ==
+ * tail_len_v[b], so the first value-tail tokens pair with the keys of pages
+ * num_pages_v[b] .. num_pages[b] - 1.  This is the KIVI split: keys are
+ * quantised per channel once G of them accumulate, values per token once
+ * they leave the FP16 local window (kitty/pipeline.py:146-177).  With
+ * num_pages_v and tail_len_v NULL, both streams use num_pages and tail_len
+ * (the contract of paged_attention_reference, which appends the FP16 tail
+ * only when it is non-empty and needs equal key / value tail lengths,
+ * kitty/kernels/attention.py:148-165).
  * out[b, qh] = softmax(q . K^T * sm_scale) V in fp16; zeros when a sequence
- * has no tokens (:180-182).
+ * has no tokens (:180-182); NaN when its lengths break the rules above.
  *
  * Pools must be the contiguous tensors of PageCentricKVLayoutManager (16-byte
  * aligned bases); page ids are int32 and byte offsets are 64-bit, so a pool
@@ -192,6 +201,11 @@ typedef struct {
 
     void *workspace;
     size_t workspace_bytes;
+
+    /* independent value stream (ABI version 2); NULL / 0 = the key stream's */
+    const int32_t *num_pages_v; /* (B,) value pages per sequence */
+    const int32_t *tail_len_v;  /* (B,) value-tail tokens per sequence, read from tail_v */
+    int32_t tail_v_capacity;    /* tokens allocated per (seq, head) in tail_v (tail_len_v set) */
 } kitty_decode_args;
 
 int kitty_decode_workspace_size(const kitty_decode_args *args, size_t *bytes);

@@ -14,8 +14,9 @@ void set_error(const std::string &msg) { g_last_error = msg; }
 const char *get_error() { return g_last_error.c_str(); }
 
 // Waves of the decode kernels resident on the current device at once:
-// waves_per_cu per CU (MFMA kernel: 8 for GQA groups of 4 and 8, with 20 KB
-// of LDS and 256 registers each, 4 for 16), 2048 / 1024 on an MI355X.
+// waves_per_cu per CU (streaming kernel: 16 for GQA groups of 4 and 8, with
+// 10 KB of LDS and 128 registers each, 8 for 16; page-pair MFMA kernel: 8
+// and 4), 4096 / 2048 on an MI355X.
 static int64_t resident_waves(int waves_per_cu = 8)
 {
     int dev = 0, cus = 0;
@@ -75,8 +76,9 @@ static void set_plan(DecodeParams &p, const kitty_decode_args &a, bool balanced)
     }
     p.pages_per_split = p.n_splits = 0;
     p.fp16_weight = fp16_weight(p.GQ);
-    p.fp16_units = seq_fp16_units(p.sink_cap + p.tail_cap, p.fp16_weight);
-    const int64_t res = resident_waves(p.GQ <= 8 ? 8 : 4);
+    p.fp16_units = seq_fp16_units(p.sink_cap + p.tail_v_cap, p.fp16_weight);
+    const bool stream = uses_stream_kernel(p);
+    const int64_t res = resident_waves(stream ? (p.GQ <= 8 ? 16 : 8) : (p.GQ <= 8 ? 8 : 4));
     if (a.pages_per_split > 0) {
         p.min_chunk = a.pages_per_split;
         const int64_t pairs = (int64_t)a.batch * a.num_kv_heads;
@@ -107,6 +109,10 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
     if (a.max_pages > 0 && (a.bt_stride < a.max_pages || !a.block_table || !a.key_low || !a.key_meta ||
                             !a.value || !a.value_meta || (a.d_boost > 0 && !a.key_high)))
         return fail(KITTY_E_INVALID, "pools and a block table with bt_stride >= max_pages are required");
+    if ((a.num_pages_v != nullptr) != (a.tail_len_v != nullptr))
+        return fail(KITTY_E_INVALID, "num_pages_v and tail_len_v go together (both NULL: one stream length)");
+    if (a.tail_len_v && a.tail_v_capacity < 0)
+        return fail(KITTY_E_INVALID, "tail_v_capacity must be >= 0");
     p = DecodeParams{};
     p.q = a.q;
     p.q_s_seq = a.q_s_seq;
@@ -130,8 +136,11 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
     p.tail_v = a.tail_v;
     p.sink_len = a.sink_len;
     p.tail_len = a.tail_len;
+    p.num_pages_v = a.num_pages_v;
+    p.tail_len_v = a.tail_len_v;
     p.sink_cap = a.sink_capacity > 0 ? a.sink_capacity : 0;
     p.tail_cap = a.tail_capacity > 0 ? a.tail_capacity : 0;
+    p.tail_v_cap = a.tail_len_v ? (a.tail_v_capacity > 0 ? a.tail_v_capacity : 0) : p.tail_cap;
     p.B = a.batch;
     p.Hq = a.num_q_heads;
     p.Hkv = a.num_kv_heads;
@@ -180,12 +189,17 @@ extern "C" int kitty_decode_workspace_size(const kitty_decode_args *args, size_t
         return rc;
     if (!bytes)
         return fail(KITTY_E_INVALID, "bytes is NULL");
-    // the size must not depend on which kernel the real pointers select
+    // the size must not depend on which kernel the real pointers select:
+    // the largest of the uniform plan and the unit-balanced plans of both
+    // MFMA kernels
     size_t n = workspace_bytes(p);
     if (mfma_shape_supported(p)) {
-        DecodeParams o = p;
-        set_plan(o, *args, !p.balanced);
-        n = std::max(n, workspace_bytes(o));
+        for (int k = 0; k < 3; ++k) {
+            DecodeParams o = p;
+            o.flags = k == 2 ? (p.flags | KITTY_DECODE_STREAM_KERNEL) : (p.flags & ~KITTY_DECODE_STREAM_KERNEL);
+            set_plan(o, *args, k != 0);
+            n = std::max(n, workspace_bytes(o));
+        }
     }
     *bytes = n;
     return KITTY_OK;

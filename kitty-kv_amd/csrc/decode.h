@@ -5,6 +5,11 @@
 namespace kitty {
 
 constexpr int kChunkMax = 256; // tokens per softmax chunk in the generic path (>= G)
+
+// Internal flags bit (not part of the public ABI): run the streaming kernel
+// for a single K/V stream too.  It always runs when the value stream is
+// independent (num_pages_v given), which the page-pair kernel does not take.
+constexpr int KITTY_DECODE_STREAM_KERNEL = 1 << 30;
 constexpr int kMaxPagesPerSplit = 64;
 
 struct DecodeParams {
@@ -25,7 +30,9 @@ struct DecodeParams {
     kitty_fp16_seg sink_k, sink_v, tail_k, tail_v;
     const int32_t *sink_len;
     const int32_t *tail_len;
-    int sink_cap, tail_cap;
+    const int32_t *num_pages_v;  // value pages per sequence; NULL: num_pages
+    const int32_t *tail_len_v;   // value tail tokens per sequence; NULL: tail_len
+    int sink_cap, tail_cap, tail_v_cap;
     int B, Hq, Hkv, GQ, D, G, Dk;
     int max_pages, pages_per_split, n_splits;
     int n_fp16;   // FP16 splits per (b, kh) of the uniform plan (one)
@@ -40,6 +47,34 @@ struct DecodeParams {
     float *ws_ml; // the same rows: running max (log2 domain) and sum
     int *ws_pair; // balanced: [B * Hkv][2] first and last partial t of each (b, kh)
 };
+
+// Stream lengths of sequence b, clamped to the buffer capacities.  The key
+// stream is sinks | npk key pages | nk key-tail tokens, the value stream
+// sinks | npv value pages | nv value-tail tokens; both cover the same tokens,
+// so the first nmix = (npk - npv) G value-tail tokens pair with the keys of
+// pages npv .. npk - 1.  Lengths that break this (or a page count outside
+// [0, max_pages], or npv > npk) mark the sequence bad: its output is NaN.
+struct SeqLens {
+    int ns, npk, npv, nk, nv, nmix;
+    bool bad;
+};
+
+__device__ __forceinline__ SeqLens seq_lens(const DecodeParams &p, int b)
+{
+    SeqLens L;
+    const int npk = p.num_pages[b];
+    const int npv = p.num_pages_v ? p.num_pages_v[b] : npk;
+    const int nk = min(max(0, p.tail_len[b]), p.tail_cap);
+    const int nv = p.tail_len_v ? min(max(0, p.tail_len_v[b]), p.tail_v_cap) : nk;
+    L.bad = npk < 0 || npk > p.max_pages || npv < 0 || npv > npk || (int64_t)(npk - npv) * p.G + nk != nv;
+    L.ns = L.bad ? 0 : min(max(0, p.sink_len[b]), p.sink_cap);
+    L.npk = L.bad ? 0 : npk;
+    L.npv = L.bad ? 0 : npv;
+    L.nk = L.bad ? 0 : nk;
+    L.nv = L.bad ? 0 : nv;
+    L.nmix = L.bad ? 0 : (npk - npv) * p.G;
+    return L;
+}
 
 // Partials per (b, query head) of the uniform plan: page splits, then FP16 splits.
 __host__ __device__ inline int num_partials(const DecodeParams &p) { return p.n_splits + p.n_fp16; }
@@ -74,6 +109,19 @@ __host__ __device__ inline int seq_fp16_units(int ntok, int weight)
 {
     return ntok > 0 ? (int)(((int64_t)ntok * weight + 127) / 128) : 0;
 }
+// Page units of sequence b (its full pages, npv: key and value both
+// quantised) and whether it is bad.
+struct SeqUnits1 {
+    int npu;
+    bool bad;
+};
+
+__device__ __forceinline__ SeqUnits1 seq_units(const DecodeParams &p, int b)
+{
+    const SeqLens L = seq_lens(p, b);
+    return SeqUnits1{seq_page_units(L.bad ? -1 : L.npv, p.max_pages, p.fp16_units), L.bad};
+}
+
 // working waves for U units: at most page_waves, each at least min_chunk units
 __host__ __device__ inline int plan_waves(int64_t U, int page_waves, int min_chunk)
 {
@@ -97,8 +145,13 @@ size_t generic_lds_bytes(int GQ, int D, int G, int Dk);
 int launch_generic(const DecodeParams &p, hipStream_t stream);
 int launch_splits(const DecodeParams &p, hipStream_t stream);
 bool mfma_shape_supported(const DecodeParams &p);
+inline bool uses_stream_kernel(const DecodeParams &p)
+{
+    return (p.flags & KITTY_DECODE_STREAM_KERNEL) || p.num_pages_v;
+}
 bool mfma_path_supported(const DecodeParams &p);
 int launch_mfma(const DecodeParams &p, hipStream_t stream);
+int launch_stream(const DecodeParams &p, hipStream_t stream);
 int launch_merge(const DecodeParams &p, hipStream_t stream);
 
 } // namespace kitty

@@ -191,14 +191,30 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
         s.brow[d] = p.boost_idx[kh * D + d];
     __syncthreads();
 
-    bool poison = false;
+    const SeqLens L = seq_lens(p, b);
+    bool poison = L.bad;
+    // key page pi staged in LDS: low / high code bits and (scale, zero) of every channel
+    auto stage_key_page = [&](int64_t ph) {
+        copy_bytes(s.klow, p.key_low + ph * D * G4, D * G4);
+        if (Dk > 0)
+            copy_bytes(s.khigh, p.key_high + ph * Dk * G4, Dk * G4);
+        for (int e = tid; e < D; e += kGenThreads) {
+            s.kscale[e] = h2f(p.key_meta[ph * 2 * D + e]);
+            s.kzero[e] = h2f(p.key_meta[ph * 2 * D + D + e]);
+        }
+    };
+    // k = ((low | high << 2) - z) * s  (dequantize_key.py:73-95)
+    auto kpage = [&](int d, int t) -> float {
+        int code = (s.klow[d * G4 + (t >> 2)] >> (2 * (t & 3))) & 3;
+        const int bi = s.brow[d];
+        if (bi < Dk)
+            code |= ((s.khigh[bi * G4 + (t >> 2)] >> (2 * (t & 3))) & 3) << 2;
+        return ((float)code - s.kzero[d]) * s.kscale[d];
+    };
     if (split < p.n_splits) {
         // ---------------------------------------------- quantised pages
-        const int np = p.num_pages[b];
-        if (np < 0 || np > p.max_pages)
-            poison = true;
         const int p0 = split * p.pages_per_split;
-        const int p1 = poison ? p0 : min(np, p0 + p.pages_per_split);
+        const int p1 = poison ? p0 : min(L.npv, p0 + p.pages_per_split);
         for (int pi = p0; pi < p1; ++pi) {
             const int32_t page = p.block_table[b * p.bt_stride + pi];
             if (page < 0 || page >= p.num_pool_pages) {
@@ -206,50 +222,52 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
                 break;
             }
             const int64_t ph = (int64_t)page * H + kh;
-            copy_bytes(s.klow, p.key_low + ph * D * G4, D * G4);
-            if (Dk > 0)
-                copy_bytes(s.khigh, p.key_high + ph * Dk * G4, Dk * G4);
+            stage_key_page(ph);
             copy_bytes(s.vcode, p.value + ph * G * D4, G * D4);
-            for (int e = tid; e < D; e += kGenThreads) {
-                s.kscale[e] = h2f(p.key_meta[ph * 2 * D + e]);
-                s.kzero[e] = h2f(p.key_meta[ph * 2 * D + D + e]);
-            }
             for (int e = tid; e < G; e += kGenThreads) {
                 s.vscale[e] = h2f(p.value_meta[ph * 2 * G + 2 * e]);
                 s.vzero[e] = h2f(p.value_meta[ph * 2 * G + 2 * e + 1]);
             }
             __syncthreads();
-            // k = ((low | high << 2) - z) * s  (dequantize_key.py:73-95)
-            auto kval = [&](int d, int t) -> float {
-                int code = (s.klow[d * G4 + (t >> 2)] >> (2 * (t & 3))) & 3;
-                const int bi = s.brow[d];
-                if (bi < Dk)
-                    code |= ((s.khigh[bi * G4 + (t >> 2)] >> (2 * (t & 3))) & 3) << 2;
-                return ((float)code - s.kzero[d]) * s.kscale[d];
-            };
             // v = (code - z_t) * s_t  (quantize_value.py:118-133)
             auto vval = [&](int t, int d) -> float {
                 const int code = (s.vcode[t * D4 + (d >> 2)] >> (2 * (d & 3))) & 3;
                 return ((float)code - s.vzero[t]) * s.vscale[t];
             };
             // G <= kChunkMax, one chunk per page
-            gen_chunk<GQ>(s, D, G, kval, vval);
+            gen_chunk<GQ>(s, D, G, kpage, vval);
         }
-    } else {
-        // ------------------------------------------ FP16 sinks then tail
-        const int ns = min(max(0, p.sink_len[b]), p.sink_cap), nt = min(max(0, p.tail_len[b]), p.tail_cap);
-        for (int seg = 0; seg < 2; ++seg) {
-            const kitty_fp16_seg &K = seg == 0 ? p.sink_k : p.tail_k;
-            const kitty_fp16_seg &V = seg == 0 ? p.sink_v : p.tail_v;
-            const int n = seg == 0 ? ns : nt;
-            const uint16_t *kb = K.ptr + b * K.s_seq + kh * K.s_head;
-            const uint16_t *vb = V.ptr + b * V.s_seq + kh * V.s_head;
-            for (int t0 = 0; t0 < n; t0 += kChunkMax) {
-                const int c = min(kChunkMax, n - t0);
-                auto kval = [&](int d, int t) -> float { return h2f(kb[(int64_t)(t0 + t) * K.s_tok + d]); };
-                auto vval = [&](int t, int d) -> float { return h2f(vb[(int64_t)(t0 + t) * V.s_tok + d]); };
-                gen_chunk<GQ>(s, D, c, kval, vval);
+    } else if (!poison) {
+        // ------------- FP16 sinks, key pages with FP16 values, key tail
+        const uint16_t *skb = p.sink_k.ptr + b * p.sink_k.s_seq + kh * p.sink_k.s_head;
+        const uint16_t *svb = p.sink_v.ptr + b * p.sink_v.s_seq + kh * p.sink_v.s_head;
+        const uint16_t *tkb = p.tail_k.ptr + b * p.tail_k.s_seq + kh * p.tail_k.s_head;
+        const uint16_t *tvb = p.tail_v.ptr + b * p.tail_v.s_seq + kh * p.tail_v.s_head;
+        for (int t0 = 0; t0 < L.ns; t0 += kChunkMax) {
+            const int c = min(kChunkMax, L.ns - t0);
+            auto kval = [&](int d, int t) -> float { return h2f(skb[(int64_t)(t0 + t) * p.sink_k.s_tok + d]); };
+            auto vval = [&](int t, int d) -> float { return h2f(svb[(int64_t)(t0 + t) * p.sink_v.s_tok + d]); };
+            gen_chunk<GQ>(s, D, c, kval, vval);
+        }
+        for (int pi = L.npv; pi < L.npk && !poison; ++pi) {
+            const int32_t page = p.block_table[b * p.bt_stride + pi];
+            if (page < 0 || page >= p.num_pool_pages) {
+                poison = true;
+                break;
             }
+            stage_key_page((int64_t)page * H + kh);
+            __syncthreads();
+            const int64_t r0 = (int64_t)(pi - L.npv) * G;  // the page's rows of the value tail
+            auto vval = [&](int t, int d) -> float { return h2f(tvb[(r0 + t) * p.tail_v.s_tok + d]); };
+            gen_chunk<GQ>(s, D, G, kpage, vval);
+        }
+        for (int t0 = 0; t0 < L.nk && !poison; t0 += kChunkMax) {
+            const int c = min(kChunkMax, L.nk - t0);
+            auto kval = [&](int d, int t) -> float { return h2f(tkb[(int64_t)(t0 + t) * p.tail_k.s_tok + d]); };
+            auto vval = [&](int t, int d) -> float {
+                return h2f(tvb[(int64_t)(L.nmix + t0 + t) * p.tail_v.s_tok + d]);
+            };
+            gen_chunk<GQ>(s, D, c, kval, vval);
         }
     }
     // ---------------------------------------------------- write partial
@@ -455,8 +473,11 @@ int launch_generic(const DecodeParams &p, hipStream_t stream)
 // for every other shape the reference accepts.
 int launch_splits(const DecodeParams &p, hipStream_t stream)
 {
-    if (mfma_path_supported(p))
+    if (mfma_path_supported(p)) {
+        if (uses_stream_kernel(p))
+            return launch_stream(p, stream);
         return launch_mfma(p, stream);
+    }
     return launch_generic(p, stream);
 }
 

@@ -18,7 +18,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 # KITTY_HIP_LIBRARY selects another build of the same ABI (e.g. a tuning variant).
 LIB_PATH = os.environ.get("KITTY_HIP_LIBRARY") or os.path.join(_HERE, "libkitty_hip.so")
 
-KITTY_ABI_VERSION = 1
+KITTY_ABI_VERSION = 2
 KITTY_OK = 0
 KITTY_E_INVALID = -1
 KITTY_E_HIP = -2
@@ -26,6 +26,7 @@ KITTY_E_UNSUPPORTED = -3
 KITTY_E_EXHAUSTED = -4
 KITTY_E_NOT_FOUND = -5
 KITTY_DECODE_UNIQUE_BOOST_ROWS = 1
+KITTY_DECODE_STREAM_KERNEL = 1 << 30  # internal: the streaming split kernel for a single K/V stream too
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -76,6 +77,7 @@ class DecodeArgs(ctypes.Structure):
         ("page_tokens", _i32), ("d_boost", _i32), ("max_pages", _i32), ("pages_per_split", _i32),
         ("flags", _i32), ("sm_scale", ctypes.c_float),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("num_pages_v", _vp), ("tail_len_v", _vp), ("tail_v_capacity", _i32),
     ]
 
 

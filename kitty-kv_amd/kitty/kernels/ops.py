@@ -159,6 +159,15 @@ class DecodePlan:
     pools as in the layout manager; boost_idx (Hkv, D) uint8;
     sink_k/v (B, Hkv, S, D) fp16 + sink_len (B,) int32;
     tail_k/v (B, Hkv, T, D) fp16 + tail_len (B,) int32; out (B, Hq, D) fp16.
+
+    Independent value stream (the KIVI split of the pipeline's FP16 value
+    window): num_pages_v (B,) int32 value pages and tail_len_v (B,) int32
+    value-tail tokens in tail_v (B, Hkv, Tv, D), with
+    (num_pages - num_pages_v) * G + tail_len == tail_len_v per sequence.
+    Without them both streams use num_pages and tail_len.
+    stream_kernel runs the streaming split kernel (the one that serves an
+    independent value stream) for a single K/V stream too, for A/B timing
+    against the page-pair kernel.
     """
 
     def __init__(self, q: torch.Tensor, block_table: torch.Tensor, num_pages: torch.Tensor,
@@ -168,9 +177,12 @@ class DecodePlan:
                  tail_k: torch.Tensor, tail_v: torch.Tensor, tail_len: torch.Tensor,
                  max_pages: Optional[int] = None, pages_per_split: int = 0,
                  sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                 workspace: Optional[torch.Tensor] = None, boost_unique: Optional[bool] = None):
+                 workspace: Optional[torch.Tensor] = None, boost_unique: Optional[bool] = None,
+                 num_pages_v: Optional[torch.Tensor] = None, tail_len_v: Optional[torch.Tensor] = None,
+                 stream_kernel: bool = False):
         dev = _hip.require_device(q, block_table, num_pages, key_baseline, key_boost, key_meta, value_pool,
                                   value_meta, boost_idx, sink_k, sink_v, sink_len, tail_k, tail_v, tail_len)
+        _need((num_pages_v is None) == (tail_len_v is None), "num_pages_v and tail_len_v go together")
         B, Hq, D = q.shape
         P, Hkv, D2, G4 = key_baseline.shape
         _need(D2 == D, "head_dim mismatch between q and pools")
@@ -183,7 +195,11 @@ class DecodePlan:
         _need(q.stride(2) == 1, "q channels must be contiguous")
         _need(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.shape[0] == B
               and block_table.stride(1) == 1, "block_table must be int32 (B, W) with contiguous rows")
-        for name, t in (("num_pages", num_pages), ("sink_len", sink_len), ("tail_len", tail_len)):
+        lens = [("num_pages", num_pages), ("sink_len", sink_len), ("tail_len", tail_len)]
+        if num_pages_v is not None:
+            _hip.require_device(num_pages_v, tail_len_v)
+            lens += [("num_pages_v", num_pages_v), ("tail_len_v", tail_len_v)]
+        for name, t in lens:
             _need(t.dtype == torch.int32 and t.numel() == B and t.is_contiguous(), f"{name} must be int32 (B,)")
         _need(boost_idx.dtype == torch.uint8 and tuple(boost_idx.shape) == (Hkv, D) and boost_idx.is_contiguous(),
               "boost_idx must be contiguous uint8 (Hkv, D)")
@@ -210,12 +226,15 @@ class DecodePlan:
         a.sink_capacity, a.tail_capacity = sink_k.shape[2], tail_k.shape[2]
         _need(sink_v.shape[2] == sink_k.shape[2] and tail_v.shape[2] >= tail_k.shape[2],
               "sink_v / tail_v must hold as many tokens as sink_k / tail_k")
+        if num_pages_v is not None:
+            a.num_pages_v, a.tail_len_v, a.tail_v_capacity = num_pages_v.data_ptr(), tail_len_v.data_ptr(), tail_v.shape[2]
         a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, D
         a.page_tokens, a.d_boost = G4 * 4, key_boost.shape[2]
         a.max_pages, a.pages_per_split = int(max_pages), int(pages_per_split)
         if boost_unique is None:
             boost_unique = boost_rows_unique(boost_idx, key_boost.shape[2])
-        a.flags = _hip.KITTY_DECODE_UNIQUE_BOOST_ROWS if boost_unique else 0
+        a.flags = (_hip.KITTY_DECODE_UNIQUE_BOOST_ROWS if boost_unique else 0) | \
+            (_hip.KITTY_DECODE_STREAM_KERNEL if stream_kernel else 0)
         a.sm_scale = float(1.0 / math.sqrt(D) if sm_scale is None else sm_scale)
         self._L = _hip.load()
         need = ctypes.c_size_t(0)
@@ -228,7 +247,8 @@ class DecodePlan:
         self.device = dev
         # keep every tensor the kernels read alive as long as the plan
         self._keep = (q, block_table, num_pages, key_baseline, key_boost, key_meta, value_pool, value_meta,
-                      boost_idx, sink_k, sink_v, sink_len, tail_k, tail_v, tail_len, workspace)
+                      boost_idx, sink_k, sink_v, sink_len, tail_k, tail_v, tail_len, workspace, num_pages_v,
+                      tail_len_v)
 
     def run(self) -> torch.Tensor:
         _hip.check(self._L.kitty_paged_decode(ctypes.byref(self.args), _hip.stream_ptr(self.device)))
@@ -248,11 +268,19 @@ def paged_decode(*args, **kwargs) -> torch.Tensor:
 
 
 def decode_workspace_bytes(B: int, Hq: int, Hkv: int, D: int, G: int, Dk: int, max_pages: int,
-                           pages_per_split: int = 0) -> int:
-    """Workspace size for paged_decode with these shapes (for preallocation)."""
+                           pages_per_split: int = 0, sink_capacity: int = 0, tail_capacity: int = 0,
+                           tail_v_capacity: Optional[int] = None) -> int:
+    """Workspace size for paged_decode with these shapes (for preallocation).
+    The FP16 buffer capacities (tokens per (sequence, head) of sink_k, tail_k
+    and, for an independent value stream, tail_v) enter the work plan, so
+    pass the ones the decode will use."""
     a = _hip.DecodeArgs()
     a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, D
     a.page_tokens, a.d_boost, a.max_pages, a.pages_per_split = G, Dk, max_pages, pages_per_split
+    a.sink_capacity, a.tail_capacity = sink_capacity, tail_capacity
+    if tail_v_capacity is not None:
+        a.num_pages_v = a.tail_len_v = 1  # non-null placeholders: an independent value stream
+        a.tail_v_capacity = tail_v_capacity
     a.bt_stride = max(1, max_pages)
     a.block_table = a.key_low = a.key_meta = a.value = a.value_meta = a.key_high = 1  # non-null placeholders
     need = ctypes.c_size_t(0)

@@ -57,11 +57,12 @@ def test_workspace_size_formula():
     from kitty.kernels.ops import decode_workspace_bytes
     row = (128 + 2) * 4  # O + (m, l) per partial row, fp32
     # Config 3 shape on 256 CUs.  Uniform plan (generic kernel): 15 splits of
-    # 17 pages + 1 FP16 split per (b, q head).  Unit-balanced plan (MFMA
-    # kernel): GQ rows per partial t < 2 (2048 resident waves + 128 pairs),
-    # plus the (first, last) partial table of the pairs.  The size covers both.
+    # 17 pages + 1 FP16 split per (b, q head).  Unit-balanced plan (streaming
+    # kernel, 16 waves per CU): GQ rows per partial t < 2 (4096 resident waves
+    # + 128 pairs), plus the (first, last) partial table of the pairs.  The
+    # size covers both.
     uniform = 16 * 32 * 16 * row
-    balanced = 2 * (2048 + 128) * 4 * row + 128 * 2 * 4
+    balanced = 2 * (4096 + 128) * 4 * row + 128 * 2 * 4
     assert decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255) == max(uniform, balanced)
     # pages_per_split = 200: uniform splits capped at 64 pages (4 + 1 per
     # head); balanced: at least 200 units per wave, 128 pairs x ceil(256 / 200)
@@ -69,6 +70,18 @@ def test_workspace_size_formula():
     uniform = 16 * 32 * (4 + 1) * row
     balanced = 2 * (128 * 2 + 128) * 4 * row + 128 * 2 * 4
     assert decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255, pages_per_split=200) == max(uniform, balanced)
+    # pages_per_split = 4: 128 pairs x ceil(units / 4) waves, where a pair's
+    # units are its pages, its FP16 units (8 per 128 sink + tail tokens of
+    # capacity) and one: the FP16 capacities enter the size
+    balanced0 = 2 * (128 * 64 + 128) * 4 * row + 128 * 2 * 4              # (255 + 0 + 1) / 4
+    balanced1 = 2 * (128 * 67 + 128) * 4 * row + 128 * 2 * 4              # (255 + 10 + 1) / 4
+    assert decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255, pages_per_split=4) == balanced0
+    assert decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255, pages_per_split=4, sink_capacity=32,
+                                  tail_capacity=128) == balanced1
+    # an independent value stream plans with the value tail's capacity (32 + 256 tokens: 18 FP16 units)
+    balanced2 = 2 * (128 * 69 + 128) * 4 * row + 128 * 2 * 4              # ceil((255 + 18 + 1) / 4)
+    assert decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255, pages_per_split=4, sink_capacity=32,
+                                  tail_capacity=128, tail_v_capacity=256) == balanced2
     # a shape only the generic kernel takes (GQA 2): uniform plan alone
     assert decode_workspace_bytes(16, 16, 8, 128, 128, 16, 255) == 16 * 16 * 16 * row
 
