@@ -218,6 +218,17 @@ int kitty_paged_decode(const kitty_decode_args *args, kitty_stream_t stream);
 int kitty_paged_decode_splits(const kitty_decode_args *args, kitty_stream_t stream);
 int kitty_paged_decode_merge(const kitty_decode_args *args, kitty_stream_t stream);
 
+/* kitty_paged_decode without a workspace: it has no counterpart in the
+ * reference and is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc).  args->workspace and workspace_bytes are ignored; the
+ * partials go to a 64 MiB array the library holds on each device it runs
+ * on, and a batch whose workspace (kitty_decode_workspace_size) exceeds it
+ * fails with KITTY_E_INVALID.  No call allocates or frees.  Every call on a
+ * device uses that device's one array: calls that overlap on one device
+ * (different streams, or different threads without ordering) race. */
+int kitty_paged_decode_noalloc(const kitty_decode_args *args, kitty_stream_t stream);
+
 /* ------------------------------------------------------ token append
  * Replaces the FP16 buffer writes of KittyInferencePipeline.push_token
  * (kitty/pipeline.py:115-181) for B sequences in one launch: sequence b's

@@ -1,6 +1,7 @@
 // C ABI entry points of libkitty_hip.so that are not kernel-specific:
 // version, error reporting, and the paged decode dispatcher.
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "common.h"
@@ -251,4 +252,55 @@ extern "C" int kitty_paged_decode(const kitty_decode_args *args, kitty_stream_t 
     if (rc)
         return rc;
     return launch_merge(p, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------ no-alloc
+// Decode workspace of kitty_paged_decode_noalloc: one copy per device,
+// held from the library's load until the process ends.  The split kernel
+// writes every partial row and pair-table entry the merge reads, so
+// nothing in it has to start at zero and no call clears it.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch[kMaxDevices];
+
+// Device address of the current device's scratch.  The array's name is a
+// host-side handle, not a device address: only the pointer returned by
+// hipGetSymbolAddress (looked up once per device, with that device
+// current) reaches kernels.
+static int scratch_address(void **out)
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return fail(KITTY_E_HIP, "hipGetDevice failed or device id out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr)
+            return fail(KITTY_E_HIP, "hipGetSymbolAddress(scratch) failed");
+        g_scratch[dev] = ptr;
+    }
+    *out = g_scratch[dev];
+    return KITTY_OK;
+}
+
+extern "C" int kitty_paged_decode_noalloc(const kitty_decode_args *args, kitty_stream_t stream)
+{
+    DecodeParams p;
+    int rc = build_params(args, p);
+    if (rc || p.B == 0)
+        return rc;
+    const size_t need = workspace_bytes(p);
+    if (need > kScratchBytes)
+        return fail(KITTY_E_INVALID, "kitty_paged_decode_noalloc: this batch needs " + std::to_string(need) +
+                                         " bytes of scratch, the maximum is " + std::to_string(kScratchBytes) +
+                                         "; use kitty_paged_decode with a workspace");
+    kitty_decode_args a = *args;
+    rc = scratch_address(&a.workspace);
+    if (rc)
+        return rc;
+    a.workspace_bytes = kScratchBytes;
+    return kitty_paged_decode(&a, stream);
 }

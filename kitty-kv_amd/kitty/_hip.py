@@ -103,7 +103,7 @@ EXPORTED_SYMBOLS = (
     "kitty_abi_version", "kitty_last_error", "kitty_quantize_kv_blocks",
     "kitty_dequantize_key_page", "kitty_dequantize_value_page",
     "kitty_decode_workspace_size", "kitty_paged_decode", "kitty_paged_decode_splits",
-    "kitty_paged_decode_merge", "kitty_append_tokens", "kitty_channel_abs_sum",
+    "kitty_paged_decode_merge", "kitty_paged_decode_noalloc", "kitty_append_tokens", "kitty_channel_abs_sum",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -132,6 +132,7 @@ def load() -> ctypes.CDLL:
     L.kitty_paged_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_paged_decode_splits.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_paged_decode_merge.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
+    L.kitty_paged_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_append_tokens.argtypes = [ctypes.POINTER(AppendArgs), _vp]
     L.kitty_channel_abs_sum.argtypes = [_vp, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _vp]
     if L.kitty_abi_version() != KITTY_ABI_VERSION:

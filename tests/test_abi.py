@@ -109,3 +109,16 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_noalloc_rejects_batches_beyond_its_scratch():
+    """kitty_paged_decode_noalloc refuses, before touching a device, a batch
+    whose workspace exceeds its fixed scratch."""
+    from kitty import _hip
+    L = _hip.load()
+    a = _hip.DecodeArgs()
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.page_tokens, a.d_boost = 20000, 32, 8, 128, 128, 16
+    a.max_pages, a.bt_stride = 255, 255
+    a.block_table = a.key_low = a.key_high = a.key_meta = a.value = a.value_meta = 1  # never dereferenced
+    assert L.kitty_paged_decode_noalloc(ctypes.byref(a), None) == _hip.KITTY_E_INVALID
+    assert b"maximum is 67108864" in L.kitty_last_error()
