@@ -11,10 +11,19 @@ through a shuffled free list.  Three independent pool copies (~953 MB) rotate
 step to step so no step is served from the 256 MB MALL.
 
 One step = one decode layer-step for all 16 sequences: kitty_paged_decode,
-i.e. the split-K kernel (pages + FP16 segments) and the merge kernel.  `value`
-is microseconds per layer-step (wall clock over K back-to-back steps, inputs
-resident in HBM); the roofline entry is for the split-K kernel, timed in a
-second pass with one HIP event pair per launch on the stream it runs on.
+i.e. the split-K kernel (pages + FP16 segments) and the merge kernel.  After
+at least --warmup steps and --warmup-seconds of them (steady clock whatever
+--steps is), `value` is microseconds per layer-step over exactly --steps
+back-to-back steps (host clock; inputs resident in HBM).  The roofline entry
+is for the split-K kernel: a second pass of the same alternating steps
+records a HIP event on the launch stream around every launch, giving each
+kernel's mean duration in the regime `value` is measured in.
+
+`legs` repeats this for configs 4 and 5, each with its own roofline block;
+`quantize_pack` times config 2's batch quantize; `cpu_baseline` is the
+reference's CPU path restated op for op in torch (oracle/torch_reference.py)
+on every thread this process may use, `cpu_baseline_c_port` the scalar C
+restatement on one thread, both on a bounded sample of the config-3 step.
 """
 from __future__ import annotations
 
@@ -131,59 +140,110 @@ def algorithmic_bytes(w) -> dict:
     return dict(per_page_head=per_page_head, packed=packed, fp16=fp16, total=packed + fp16 + small)
 
 
-def cpu_baseline(w, budget_s: float) -> dict:
-    """Oracle C port of paged_attention_reference, one thread, on whole
-    sequences of the same workload until ~budget_s of CPU work."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import numpy as np
-    import oracle as O
-    O.build()
+def cpu_threads() -> int:
+    """Threads for the torch CPU baseline: every CPU this process may run on,
+    capped by OMP_NUM_THREADS when the host sets it (a GPU box's CPU share)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(cap))) if cap.isdigit() and int(cap) > 0 else max(1, n)
+
+
+def _cpu_sequences(w, budget_s: float, run_one) -> dict:
+    """Whole sequences of the workload through run_one(b, sub-pools) until
+    about budget_s of CPU time; the total is scaled by pages to one
+    layer-step (the reference's time is linear in the pages it walks)."""
     kb, kh, km, vp, vm = w["pools"]
     bt = w["tables"][0]
     done, t_total, pages_done = 0, 0.0, 0
     while done < w["B"] and (t_total < budget_s or done == 0):
         b = done
-        npb, n = w["np_list"][b], w["tail_list"][b]
+        npb = w["np_list"][b]
         idx = bt[b, :npb].long()
-        sub = [t[idx].cpu().numpy() for t in (kb, kh, km, vp, vm)]
-        args = (w["q"][b].cpu().numpy(), np.arange(npb, dtype=np.int32), *sub, w["bi"].cpu().numpy(),
-                w["dk"], w["sk"][b].cpu().numpy(), w["sv"][b].cpu().numpy(), w["tk"][b, :, :n].cpu().numpy(),
-                w["tv"][b, :, :n].cpu().numpy(), w["Hq"], w["Hkv"], D)
+        sub = [t[idx].cpu() for t in (kb, kh, km, vp, vm)]   # the sequence's pages, compacted on the host
         t0 = time.perf_counter()
-        # the reference's first pass over the pages (attention.py:100-132)
-        # dequantises every (page, head) and discards the result
-        skb, skh, skm, svp, svm = sub
-        bin_ = args[7]
-        for pg in range(npb):
-            for h in range(w["Hkv"]):
-                O.dequantize_key(skb[pg, h], skh[pg, h], skm[pg, h, 0], skm[pg, h, 1], bin_[h], w["dk"])
-                O.dequantize_value(svp[pg, h], svm[pg, h, :, 0], svm[pg, h, :, 1])
-        O.paged_attention(*args, n_threads=1)
+        run_one(b, sub)
         t_total += time.perf_counter() - t0
         done += 1
         pages_done += npb
-    # scale by pages: the oracle's time is linear in the pages it walks
     total_pages = sum(w["np_list"])
-    value = t_total * total_pages / max(pages_done, 1)
-    return {"value": round(value * 1e6, 1), "unit": "us/layer-step", "cores": 1, "kind": "port", **host_cpu(),
-            "sample": f"{done} of {w['B']} sequences ({pages_done} of {total_pages} pages, all {w['Hkv']} KV heads, "
-                      f"{S} sinks + FP16 tail each) through oracle/kitty_oracle.c (paged_attention_reference "
-                      f"restated, with its discarded first dequantisation pass), single thread; scaled by pages "
-                      f"to one layer-step"}
+    return dict(value=t_total * total_pages / max(pages_done, 1), done=done, pages_done=pages_done,
+                total_pages=total_pages)
+
+
+def cpu_baseline_torch(w, budget_s: float) -> dict:
+    """The reference's own CPU path, restated op for op in torch
+    (oracle/torch_reference.py: paged_attention_reference with its discarded
+    first dequantisation pass and per-channel high-bit loop), on whole
+    sequences of the workload, with every thread torch may use here."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import torch
+    import torch_reference as TR
+    threads = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    q, sk, sv, tk, tv, bi = (t.cpu() for t in (w["q"], w["sk"], w["sv"], w["tk"], w["tv"], w["bi"]))
+
+    def run_one(b, sub):
+        n = w["tail_list"][b]
+        TR.paged_attention(q[b], range(w["np_list"][b]), *sub, bi, w["dk"], sk[b], sv[b], tk[b, :, :n],
+                           tv[b, :, :n], w["Hq"], w["Hkv"], D)
+    try:
+        r = _cpu_sequences(w, budget_s, run_one)
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": round(r["value"] * 1e6, 1), "unit": "us/layer-step", "cores": threads, "kind": "port",
+            **host_cpu(),
+            "sample": f"{r['done']} of {w['B']} sequences ({r['pages_done']} of {r['total_pages']} pages, all "
+                      f"{w['Hkv']} KV heads, {S} sinks + FP16 tail each) through oracle/torch_reference.py "
+                      f"(paged_attention_reference restated op for op in torch, CPU, {threads} threads); "
+                      f"scaled by pages to one layer-step"}
+
+
+def cpu_baseline_c(w, budget_s: float) -> dict:
+    """The scalar C restatement (oracle/kitty_oracle.c) of the same function,
+    one thread, for comparison with the torch figure."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    O.build()
+    bin_ = w["bi"].cpu().numpy()
+    q, sk, sv, tk, tv = (t.cpu().numpy() for t in (w["q"], w["sk"], w["sv"], w["tk"], w["tv"]))
+
+    def run_one(b, sub):
+        skb, skh, skm, svp, svm = [t.numpy() for t in sub]
+        npb, n = w["np_list"][b], w["tail_list"][b]
+        for pg in range(npb):            # the reference's discarded first pass (attention.py:100-132)
+            for h in range(w["Hkv"]):
+                O.dequantize_key(skb[pg, h], skh[pg, h], skm[pg, h, 0], skm[pg, h, 1], bin_[h], w["dk"])
+                O.dequantize_value(svp[pg, h], svm[pg, h, :, 0], svm[pg, h, :, 1])
+        O.paged_attention(q[b], np.arange(npb, dtype=np.int32), skb, skh, skm, svp, svm, bin_, w["dk"], sk[b],
+                          sv[b], tk[b, :, :n], tv[b, :, :n], w["Hq"], w["Hkv"], D, n_threads=1)
+    r = _cpu_sequences(w, budget_s, run_one)
+    return {"value": round(r["value"] * 1e6, 1), "unit": "us/layer-step", "cores": 1, "kind": "port",
+            **host_cpu(),
+            "sample": f"{r['done']} of {w['B']} sequences ({r['pages_done']} of {r['total_pages']} pages) through "
+                      f"oracle/kitty_oracle.c (paged_attention_reference restated in scalar C, with its "
+                      f"discarded first pass), single thread; scaled by pages to one layer-step"}
 
 
 def host_cpu() -> dict:
-    """Host CPU of this run: model string and the threads the OS offers."""
-    model = "unknown"
+    """Host CPU of this run: /proc/cpuinfo's model string with its family,
+    model and stepping numbers (a virtualised host may shorten the string),
+    and the threads the OS offers."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                if not line.strip():
+                    break                      # first processor only
+                k, _, v = line.partition(":")
+                info[k.strip()] = v.strip()
     except OSError:
         pass
-    return {"cpu_model": model, "host_threads": os.cpu_count()}
+    model = info.get("model name", "unknown")
+    ident = "family {} model {} stepping {}".format(info.get("cpu family", "?"), info.get("model", "?"),
+                                                    info.get("stepping", "?"))
+    return {"cpu_model": f"{model} ({info.get('vendor_id', '?')} {ident})", "host_threads": os.cpu_count()}
 
 
 def quantize_cpu_baseline(k, v, bi, dk: int) -> dict:
@@ -278,17 +338,122 @@ def copy_probe(torch, dev) -> int:
     return 0
 
 
+def time_decode(torch, plans, steps: int, warm_steps: int, warm_s: float) -> dict:
+    """Steady-state timing of kitty_paged_decode steps (split + merge).
+
+    Warm-up: at least warm_steps steps and warm_s seconds of them, so the GPU
+    clock has settled whatever --steps is.  `value`: exactly `steps`
+    back-to-back steps between two HIP events and by the host clock.  The
+    split / merge breakdown comes from a second pass of the same alternating
+    steps (at least 200) with an event recorded on the launch stream before
+    each split, between split and merge, and after each merge: per-launch
+    durations in the regime `value` is measured in.  An event pair adds its
+    marker gap to the launch it brackets, so these are upper bounds of the
+    kernel times (the rocprofv3 trace gives the bare ones)."""
+    n = len(plans)
+    t_end = time.perf_counter() + warm_s
+    i = 0
+    while i < warm_steps or time.perf_counter() < t_end:
+        plans[i % n].run()
+        i += 1
+        if i % 256 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    warm_done = i
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        plans[i % n].run()
+    e1.record()
+    torch.cuda.synchronize()
+    wall_us = (time.perf_counter() - t0) * 1e6 / steps
+    event_us = e0.elapsed_time(e1) * 1e3 / steps
+    m = max(steps, 200)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * m + 1)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for i in range(m):
+        p = plans[i % n]
+        p.run_splits()
+        ev[2 * i + 1].record()
+        p.run_merge()
+        ev[2 * i + 2].record()
+    torch.cuda.synchronize()
+    split = [ev[2 * i].elapsed_time(ev[2 * i + 1]) * 1e3 for i in range(m)]
+    merge = [ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) * 1e3 for i in range(m)]
+    step_inst = ev[0].elapsed_time(ev[2 * m]) * 1e3 / m
+    kernel_us = sum(split) / m
+    merge_us = sum(merge) / m
+    assert kernel_us <= step_inst, (kernel_us, step_inst)
+    return dict(wall_us=wall_us, event_us=event_us, kernel_us=kernel_us, merge_us=merge_us,
+                kernel_median_us=statistics.median(split), merge_median_us=statistics.median(merge),
+                step_instrumented_us=step_inst, instrumented_steps=m, warm_steps=warm_done, warm_s=warm_s)
+
+
+def decode_leg(torch, dev, name: str, copies: int, placement: str, steps: int, warm_steps: int,
+               warm_s: float, keep: bool = False):
+    """One decode workload: build it, time it, return (record, workload)."""
+    cfg = CONFIGS[name]
+    log(f"building {name} workload ({copies} pool copies)")
+    w = build_workload(torch, dev, cfg, copies, placement)
+    nb = algorithmic_bytes(w)
+    log(f"{name}: pool {w['P']} pages, {nb['packed'] / 1e6:.1f} MB packed KV per step")
+    t = time_decode(torch, w["plans"], steps, warm_steps, warm_s)
+    log(f"{name}: {t['wall_us']:.1f} us/step wall ({t['event_us']:.1f} by events); split kernel "
+        f"{t['kernel_us']:.1f} us, merge {t['merge_us']:.1f} us (instrumented step {t['step_instrumented_us']:.1f})")
+    kernel_us = t["kernel_us"]
+    achieved = nb["total"] / (kernel_us * 1e-6) / 1e9
+    packed_gbps = nb["packed"] / (kernel_us * 1e-6) / 1e9
+    step_packed = nb["packed"] / (t["wall_us"] * 1e-6) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"decode_{name}_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    GQ = cfg["Hq"] // cfg["Hkv"]
+    rec = {
+        "value": round(t["wall_us"], 2), "unit": "us/layer-step", "step_us_events": round(t["event_us"], 2),
+        "workload": f"{name}: B{cfg['B']} Hq{cfg['Hq']} Hkv{cfg['Hkv']} d{D} ctx{cfg['ctx']} S{S} G{G} "
+                    f"{int(cfg['boost'] * 100 * 10) / 10}% INT4 keys, INT2 values",
+        "pages_per_seq": w["n_pages"] if len(set(w["np_list"])) == 1 else sum(w["np_list"]) / cfg["B"],
+        "tail_tokens": w["n_tail"], "pool_copies": len(w["plans"]),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "kernel": f"decode_mfma_kernel<{GQ}> (split-K phase of kitty_paged_decode)",
+                     "kernel_us": round(kernel_us, 2), "merge_us": round(t["merge_us"], 2),
+                     "kernel_median_us": round(t["kernel_median_us"], 2),
+                     "merge_median_us": round(t["merge_median_us"], 2),
+                     "step_instrumented_us": round(t["step_instrumented_us"], 2),
+                     "instrumented_steps": t["instrumented_steps"], "warmup_steps": t["warm_steps"],
+                     "warmup_s": t["warm_s"],
+                     "algorithmic_bytes": nb["total"], "packed_kv_bytes": nb["packed"],
+                     "packed_kv_GBps": round(packed_gbps, 1),
+                     "packed_kv_frac": round(packed_gbps / HBM_PEAK_GBPS, 4),
+                     "step_packed_kv_frac": round(step_packed / HBM_PEAK_GBPS, 4)},
+    }
+    return rec, (w if keep else None)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup-seconds", type=float, default=1.0,
+                    help="minimum seconds of decode steps before any timing (per leg)")
     ap.add_argument("--config", choices=sorted(CONFIGS), default="cfg3")
+    ap.add_argument("--legs", default="cfg4,cfg5",
+                    help="other decode configs timed after the main one, each with its own roofline "
+                         "('' for none)")
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--placement", choices=["shuffled", "first-fit"], default="shuffled",
                     help="page ids: a shuffled free list (fragmented pool) or first-fit order of B sequences "
                          "growing in lockstep")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-quantize", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
@@ -307,92 +472,47 @@ def main() -> int:
     if args.copy_probe:
         return copy_probe(torch, dev)
     cfg = CONFIGS[args.config]
-    log(f"building {args.config} workload ({args.copies} pool copies)")
-    w = build_workload(torch, dev, cfg, args.copies, args.placement)
-    nb = algorithmic_bytes(w)
-    plans = w["plans"]
-    log(f"pool {w['P']} pages, {nb['packed'] / 1e6:.1f} MB packed KV per step; warmup {args.warmup}")
-    for i in range(args.warmup):
-        plans[i % len(plans)].run()
-    torch.cuda.synchronize()
-
+    main_rec, w = decode_leg(torch, dev, args.config, args.copies, args.placement, args.steps, args.warmup,
+                             args.warmup_seconds, keep=not args.no_cpu_baseline)
     K = args.steps
-    # kernel durations: bursts of K back-to-back launches of the split kernel
-    # (the dominant one), then of the merge kernel, each burst between two HIP
-    # events on the launch stream (an event pair per launch would add the
-    # dispatch latency of every launch to the kernel time).  The median of
-    # five bursts: the first one after start-up can run while the GPU clock
-    # is still rising.
-    def burst(fn) -> float:
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        a.record()
-        for i in range(K):
-            fn(plans[i % len(plans)])
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / K * 1e3
-    kernel_us = statistics.median(burst(lambda p: p.run_splits()) for _ in range(5))
-    merge_us = statistics.median(burst(lambda p: p.run_merge()) for _ in range(5))
-    # whole-job rate, timed last (the GPU at its steady clock): K back-to-back
-    # decode steps between two HIP events
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record()
-    for i in range(K):
-        plans[i % len(plans)].run()
-    e1.record()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / K
-    step_us_events = e0.elapsed_time(e1) / K * 1e3
-    log(f"{ms_per_step * 1e3:.1f} us/step wall ({step_us_events:.1f} by events); "
-        f"split kernel {kernel_us:.1f} us, merge {merge_us:.1f} us")
-    achieved = nb["total"] / (kernel_us * 1e-6) / 1e9
-    packed_gbps = nb["packed"] / (kernel_us * 1e-6) / 1e9
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"decode_{args.config}_traffic.json")
-    if os.path.exists(tpath):
-        try:
-            traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
-
     result = {
         "metric": "decode-attn µs/layer + achieved HBM GB/s (% peak), 32Q/8KV d128 b16 32K ctx"
         if args.config == "cfg3" else f"decode-attn us/layer-step ({args.config})",
-        "value": round(ms_per_step * 1e3, 2),
+        "value": main_rec["value"],
         "unit": "us/layer-step",
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(main_rec["value"] / 1e3, 4),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic: fp16 N(0,1) K/V with x{:g} outlier key channels, quantised on device".format(
             cfg["outlier"]),
-        "config": {"workload": f"{args.config}: B{cfg['B']} Hq{cfg['Hq']} Hkv{cfg['Hkv']} d{D} ctx{cfg['ctx']} "
-                               f"S{S} G{G} {int(cfg['boost'] * 100 * 10) / 10}% INT4 keys, INT2 values",
-                   "batch": cfg["B"], "context": cfg["ctx"] if not isinstance(cfg["ctx"], tuple) else list(cfg["ctx"]),
-                   "pages_per_seq": w["n_pages"] if len(set(w["np_list"])) == 1 else sum(w["np_list"]) / cfg["B"],
-                   "tail_tokens": w["n_tail"], "pool_copies": len(plans), "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": f"decode_mfma_kernel<{cfg['Hq'] // cfg['Hkv']}> (split-K phase of kitty_paged_decode)",
-                     "kernel_us": round(kernel_us, 2), "merge_us": round(merge_us, 2),
-                     "step_us_events": round(step_us_events, 2),
-                     "algorithmic_bytes": nb["total"], "packed_kv_bytes": nb["packed"],
-                     "packed_kv_GBps": round(packed_gbps, 1),
-                     "packed_kv_frac": round(packed_gbps / HBM_PEAK_GBPS, 4)},
+        "config": {"workload": main_rec["workload"], "batch": cfg["B"],
+                   "context": cfg["ctx"] if not isinstance(cfg["ctx"], tuple) else list(cfg["ctx"]),
+                   "pages_per_seq": main_rec["pages_per_seq"], "tail_tokens": main_rec["tail_tokens"],
+                   "pool_copies": main_rec["pool_copies"], "parallelism": "single GPU"},
+        "step_us_events": main_rec["step_us_events"],
+        "roofline": main_rec["roofline"],
     }
+    if not args.no_cpu_baseline:
+        log(f"timing CPU baselines ({cpu_threads()} torch threads, then the C port on 1 thread)")
+        result["cpu_baseline"] = cpu_baseline_torch(w, args.cpu_seconds)
+        result["cpu_baseline_c_port"] = cpu_baseline_c(w, args.cpu_seconds * 2 / 3)
+    del w
+    torch.cuda.empty_cache()
+    legs = {}
+    for name in [x for x in args.legs.split(",") if x and x != args.config]:
+        rec, _ = decode_leg(torch, dev, name, args.copies, args.placement, K, args.warmup,
+                            max(0.5, args.warmup_seconds / 2))
+        legs[name] = rec
+        torch.cuda.empty_cache()
+    if legs:
+        result["legs"] = legs
     if not args.no_quantize:
         result["quantize_pack"] = bench_quantize(torch, dev, cpu=not args.no_cpu_baseline)
-    if not args.no_cpu_baseline:
-        log("timing CPU baseline (oracle port, 1 thread)")
-        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0
 

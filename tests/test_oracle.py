@@ -286,3 +286,31 @@ def test_zero_point_sign_follows_torch_minimum_maximum():
     zvt = torch.minimum(torch.maximum(zr, torch.zeros_like(zr)), torch.full_like(zr, 3.0)).half()
     for _, _, z_ in (O.quantize_value(v), O.quantize_value_np(v)):
         assert np.array_equal(np.asarray(z_).view(np.uint16), zvt.numpy().view(np.uint16))
+
+
+def test_torch_restatement_matches_c_oracle():
+    """oracle/torch_reference.py (the timed CPU baseline) against the C
+    oracle: dequantised pages bit for bit (same fp32 operations), the decode
+    output to within the fp32 summation order (a few fp16 ulp)."""
+    import torch_reference as TR
+    rng = np.random.default_rng(21)
+    H, Hq, D, G, dk = 2, 8, 32, 16, 6
+    c = make_paged_case(rng, H, Hq, D, G, dk, 3, 4, 5)
+    t = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in c.items() if isinstance(v, np.ndarray)}
+    for p in c["pages"]:
+        for h in range(H):
+            ref_k = O.dequantize_key(c["kb"][p, h], c["kh"][p, h], c["km"][p, h, 0], c["km"][p, h, 1], c["bi"][h], dk)
+            got_k = TR.dequantize_key_page(t["kb"][p, h], t["kh"][p, h], t["km"][p, h, 0], t["km"][p, h, 1],
+                                           t["bi"][h], dk).numpy()
+            assert np.array_equal(got_k.view(np.uint32), np.asarray(ref_k, np.float32).view(np.uint32))
+            ref_v = O.dequantize_value(c["vp"][p, h], c["vm"][p, h, :, 0], c["vm"][p, h, :, 1])
+            got_v = TR.dequantize_value_page(t["vp"][p, h], t["vm"][p, h, :, 0], t["vm"][p, h, :, 1]).numpy()
+            assert np.array_equal(got_v.view(np.uint32), np.asarray(ref_v, np.float32).view(np.uint32))
+    ref = O.paged_attention(c["q"], c["pages"], c["kb"], c["kh"], c["km"], c["vp"], c["vm"], c["bi"], dk,
+                            c["sk"], c["sv"], c["tk"], c["tv"], Hq, H, D)
+    got = TR.paged_attention(t["q"], [int(p) for p in c["pages"]], t["kb"], t["kh"], t["km"], t["vp"], t["vm"],
+                             t["bi"], dk, t["sk"], t["sv"], t["tk"], t["tv"], Hq, H, D).numpy()
+    assert np.allclose(got.astype(np.float32), ref.astype(np.float32), atol=2e-3, rtol=2e-3)
+    empty = TR.paged_attention(t["q"], [], t["kb"], t["kh"], t["km"], t["vp"], t["vm"], t["bi"], dk,
+                               t["sk"][:, :0], t["sv"][:, :0], t["tk"][:, :0], t["tv"][:, :0], Hq, H, D)
+    assert (empty.float() == 0).all()
