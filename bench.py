@@ -53,7 +53,11 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_workload(torch, dev, cfg, copies: int, placement_kind: str = "shuffled"):
+def build_workload(torch, dev, cfg, copies: int, placement_kind: str = "shuffled", sample_pages=()):
+    """Pools of `copies` independent copies of the config's KV, quantised on
+    the device from seeded fp16 K/V, with one DecodePlan per copy.  The fp16
+    inputs of the pool pages in sample_pages are kept (w["samples"][page] =
+    (k, v), each (Hkv, G, D) on the host) for parity checks."""
     from kitty.kernels.ops import DecodePlan, pool_store, quantize_into_pools
     import numpy as np
     B, Hq, Hkv = cfg["B"], cfg["Hq"], cfg["Hkv"]
@@ -98,11 +102,16 @@ def build_workload(torch, dev, cfg, copies: int, placement_kind: str = "shuffled
     for h in range(Hkv):
         scale[h, chans[h].to(dev)] = cfg["outlier"]
     chunk = 1024
+    samples = {}
+    want = {int(x) for x in sample_pages}
     for p0 in range(0, used, chunk):
         n = min(chunk, used - p0)
         k = (torch.randn(n, Hkv, G, D, device=dev, generator=g) * scale[None, :, None, :]).half()
         v = torch.randn(n, Hkv, G, D, device=dev, generator=g).half()
         quantize_into_pools(store, k, v, bi, placement[p0:p0 + n].to(dev), sentinel)
+        for i, pid in enumerate(placement[p0:p0 + n].tolist()):
+            if pid in want:
+                samples[pid] = (k[i].cpu(), v[i].cpu())
     torch.cuda.synchronize()
 
     q = torch.randn(B, Hq, D, device=dev, generator=g).half()
@@ -126,7 +135,7 @@ def build_workload(torch, dev, cfg, copies: int, placement_kind: str = "shuffled
         plans.append(DecodePlan(q, bt, npg, kb, kh, km, vp, vm, bi, sk, sv, sl, tk, tv, tl, out=out))
     w = dict(B=B, Hq=Hq, Hkv=Hkv, dk=dk, n_pages=n_pages, n_tail=n_tail, np_list=np_list, tail_list=tail_list,
              P=P, pools=(kb, kh, km, vp, vm), tables=tables, q=q, sk=sk, sv=sv, tk=tk, tv=tv, bi=bi, plans=plans,
-             out=out)
+             out=out, sentinel=sentinel, samples=samples)
     return w
 
 

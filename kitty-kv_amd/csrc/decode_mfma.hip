@@ -8,18 +8,19 @@
 // (page, head) record from HBM into a 10 KB LDS stage one page ahead, and:
 //
 //  QK   S[h][t] = sum_k A[h][k] * B[k][t] with v_mfma_f32_16x16x32_f16.
-//       B: 2-bit codes turned into fp16 by OR-ing them into the mantissa of
-//       1024: the code of token slot a (bits 2a, 2a+1 of a byte) masked in
-//       place gives 1024 + 4^a c exactly, one v_and_or_b32 per two codes, the
-//       odd bytes of each word after one shift by 8.  ds_read_b64_tr_b8
-//       transposes the channel-major page in LDS so each lane holds 8
-//       channels of one byte column (4 tokens, one per slot a).
-//       A: q * scale_k[d] * log2(e)/sqrt(D) (fp16), heads on MFMA rows.
-//       Every MFMA of slot a accumulates 4^a sum_k A[k] c plus
-//       1024 sum_k A[k]; each tile starts from -1024 sum_k A[k] (bias tile
-//       X), the softmax scales it by 4^-a and subtracts Y = sum_k A[k] z_k
-//       (bias tile Y; 9 bias MFMAs in all).  High 2 bits of boosted channels
-//       are 16-32 extra reduction rows with A = 4 * q'[channel(rank)].
+//       B: 2-bit codes as fp16 subnormals: the code of token slot a (bits
+//       2a, 2a+1 of a byte) masked in place is c 4^a 2^-24 exactly, one
+//       v_and_b32 per two codes, the odd bytes of each word after one shift
+//       by 8.  ds_read_b64_tr_b8 transposes the channel-major page in LDS so
+//       each lane holds 8 channels of one byte column (4 tokens, one per
+//       slot a).
+//       A: q * scale_k[d] on two MFMA rows per head, the fp16-rounded
+//       product and its exact residual (qk_residual), so the scores keep
+//       fp32 accuracy; sm_scale * log2(e) multiplies the scores.
+//       Every MFMA of slot a accumulates 4^a 2^-24 sum_k A[k] c; the softmax
+//       scales it by 2^24 4^-a and subtracts Y = sum_k A[k] z_k (bias tile Y,
+//       4-5 MFMAs).  High 2 bits of boosted channels are 16-32 extra
+//       reduction rows with A = 4 q[channel(rank)] scale_k.
 //  softmax  online, base 2, one DPP row reduction per page.
 //  PV, GQA 4: v_mfma_f32_16x16x128_f8f6f4 with the value codes as fp4 B
 //       operands (ds_read_b64_tr_b4 + one mask per 8 codes) and P' as three
@@ -27,16 +28,17 @@
 //       8 MFMAs per page instead of 32.
 //  PV, GQA 8 / 16: O[h][d] = sum_t P'[h][t] * B[t][d], P' = p * s_t (fp16) staged
 //       through a 1-2 KB LDS buffer; value codes get the same tr8 + mask
-//       treatment, so output tile a (channel slot a) accumulates 4^a O plus
-//       1024 sum_t P'; the per-token zero points and the 1024 offsets are
-//       subtracted from the accumulator at each page, and the 4^a is
-//       divided out when the segment's partial is written.
+//       treatment, so output tile a (channel slot a) accumulates
+//       4^a 2^-24 sum_t P' c; the per-token zero points are subtracted in
+//       those units at each page, and 2^24 4^-a is applied when the
+//       segment's partial is written.
 //
 // Reduction index k of every MFMA follows the natural channel / token order
 // within a 32-wide step (the tr8 row order puts even and odd bytes of a
 // word on consecutive k).
 #include "common.h"
 #include "decode.h"
+#include "qk_exact.h"
 
 namespace kitty {
 
@@ -70,24 +72,6 @@ __device__ __forceinline__ i32x2 tr8(const unsigned char *lds)
     return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2 *)lds);
 }
 
-// Slot `a` (token 4j+a of a key byte, or channel 4j+a of a value byte) of
-// the 8 transposed bytes -> 8 fp16 MFMA inputs 1024 + 4^a c: the even bytes
-// of each word are masked in place, the odd bytes after the word was shifted
-// right by 8 (done once per word, shared by the four slots).  The masks live
-// in VGPRs (see CodeMasks) so each half pair is one v_and_or_b32; gfx9 VOP3
-// cannot encode two literal operands.
-struct CodeMasks {
-    unsigned slot[4];  // 0x00030003 << 2a
-    unsigned one;      // 0x64006400
-};
-
-__device__ __forceinline__ CodeMasks code_masks()
-{
-    CodeMasks m{{0x00030003u, 0x000C000Cu, 0x00300030u, 0x00C000C0u}, 0x64006400u};
-    asm volatile("" : "+v"(m.slot[0]), "+v"(m.slot[1]), "+v"(m.slot[2]), "+v"(m.slot[3]), "+v"(m.one));
-    return m;
-}
-
 // A tr8 result and its odd bytes moved down: {w0, w1, w0 >> 8, w1 >> 8}.
 struct RawCodes {
     unsigned w[4];
@@ -98,15 +82,31 @@ __device__ __forceinline__ RawCodes raw_codes(i32x2 raw)
     return RawCodes{{(unsigned)raw[0], (unsigned)raw[1], (unsigned)raw[0] >> 8, (unsigned)raw[1] >> 8}};
 }
 
+// Slot `a` (token 4j+a of a key byte, or channel 4j+a of a value byte) of
+// the 8 transposed bytes -> 8 fp16 MFMA inputs: the code masked in place is
+// the fp16 subnormal c 4^a 2^-24, exactly, one v_and_b32 per two codes (the
+// odd bytes of each word after one shift by 8, shared by the four slots).
+// The MFMA sums then hold only the signal, 4^a 2^-24 sum A c, which keeps
+// full fp32 accuracy (an offset would cancel in the accumulator); the
+// consumers scale slot a by 2^24 / 4^a.
+constexpr float kSub = 16777216.0f;  // 2^24
+
 template <int A>
-__device__ __forceinline__ half8 codes_to_half8(const RawCodes &r, const CodeMasks &m)
+__device__ __forceinline__ half8 codes_to_half8(const RawCodes &r)
 {
+    constexpr unsigned m = 0x00030003u << (2 * A);
     u32x4 v;
-    v[0] = (r.w[0] & m.slot[A]) | m.one;
-    v[1] = (r.w[2] & m.slot[A]) | m.one;
-    v[2] = (r.w[1] & m.slot[A]) | m.one;
-    v[3] = (r.w[3] & m.slot[A]) | m.one;
+    v[0] = r.w[0] & m;
+    v[1] = r.w[2] & m;
+    v[2] = r.w[1] & m;
+    v[3] = r.w[3] & m;
     return __builtin_bit_cast(half8, v);
+}
+
+__device__ __forceinline__ half8 slot_codes(const RawCodes &r, int a)
+{
+    return a == 0 ? codes_to_half8<0>(r) : a == 1 ? codes_to_half8<1>(r) : a == 2 ? codes_to_half8<2>(r)
+                                                                                  : codes_to_half8<3>(r);
 }
 
 // PV operands of the GQA-4 path (v_mfma_f32_16x16x128_f8f6f4, A fp8 e4m3,
@@ -197,6 +197,7 @@ __device__ __forceinline__ unsigned pack_h2(float a, float b)
 __device__ __forceinline__ half2v as_h2(unsigned u) { return __builtin_bit_cast(half2v, u); }
 __device__ __forceinline__ unsigned as_u(half2v h) { return __builtin_bit_cast(unsigned, h); }
 
+
 struct PageSrc {
     const unsigned char *klo, *val, *khi, *kmeta, *vmeta;
 };
@@ -251,8 +252,9 @@ __device__ __forceinline__ void wait_vmcnt()
 // step.  The step's K and V rows stream into the two LDS stages with
 // global_load_lds (no registers hold data in flight): K chunk c of token row n
 // is stored at chunk c ^ (n & 15), so the 16 rows one MFMA B read touches hit
-// 16 different bank groups.  QK: f16 MFMAs with the heads on rows (A = q *
-// sm_scale * log2(e) in fp16, B = K rows), base-2 online softmax per head row
+// 16 different bank groups.  QK: f16 MFMAs with the heads on rows (A = q,
+// B = K rows, exact products; scores times sm_scale log2(e) in fp32), base-2
+// online softmax per head row
 // with DPP row reductions, P through LDS.  PV: VALU, lane = channel pair.
 // Returns each head's (m, l) and O (channels 2 lane, 2 lane + 1).
 template <int GQ>
@@ -264,19 +266,19 @@ __device__ void fp16_segments(const DecodeParams &p, int b, int kh, int lo, int 
     float *pbuf = (float *)(vst + kTok * 256);  // [head][token] fp32, GQ * 32 floats
     // A operand: row r = head r (rows past GQ are zero), k = 8 kq + i of each
     // 32-channel step
+    // (fp16 q as is: q k is exact in the fp32 accumulator, and the scores
+    // are scaled by sm_scale log2(e) afterwards)
     half8 qa[4];
+    const float qk_c = p.sm_scale * kLog2e;
     {
-        const float qscale = p.sm_scale * kLog2e;
         const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + (r < GQ ? r : 0)) * p.q_s_head;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const u32x4 raw = *(const u32x4 *)(qrow + 32 * s + 8 * kq);
             u32x4 v;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const half2v h = as_h2(raw[j]);
-                v[j] = r < GQ ? pack_h2((float)h[0] * qscale, (float)h[1] * qscale) : 0u;
-            }
+            for (int j = 0; j < 4; ++j)
+                v[j] = r < GQ ? raw[j] : 0u;
             qa[s] = __builtin_bit_cast(half8, v);
         }
     }
@@ -319,6 +321,9 @@ __device__ void fp16_segments(const DecodeParams &p, int b, int kh, int lo, int 
                 const half8 kb = *(const half8 *)(kst + 256 * n + 16 * ((4 * s + kq) ^ r));
                 S[tg] = mfma(qa[s], kb, S[tg]);
             }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                S[tg][i] *= qk_c;
         }
         // ---- online softmax per head row (tokens past cnt masked)
         float alpha[4];
@@ -378,7 +383,8 @@ __device__ void fp16_segments(const DecodeParams &p, int b, int kh, int lo, int 
 template <int GQ>
 struct WaveState {
     static constexpr int HPL = GQ / 4;      // heads per lane group
-    u32x4 qv[4], qvh;                        // static halves of the QK A operand
+    u32x4 qv[4], qvh;                        // static halves of the QK A operand (fp16 q)
+    float qk_c;                              // sm_scale * log2(e): scores in log2 units
     int hch[8];                              // channel of high-bit row 8q + i
     int tr_base0, tr_base1;                  // tr8 source offsets (byte columns 0-15 / 16-31)
     int prow;                                // head row whose P' this lane reads for PV
@@ -386,7 +392,6 @@ struct WaveState {
     f32x4 O[2][4];                           // GQA 8 / 16: output tiles (4^a O of channels 64cb + 4r + a)
     float o4[4][2];                          // GQA 4: O of head q, channels 32ch + 2r + e
     int trv[2][2];                           // GQA 4: tr4 offsets of value rows 32q + 16k + r, 16-byte chunk c
-    CodeMasks cm;                            // set once per wave: kept in VGPRs, not rebuilt per page
 };
 
 // GQA 4: online softmax and PV of one page with fp8 x fp4 MFMAs.  Lane
@@ -416,19 +421,21 @@ __device__ __forceinline__ void pv_fp8_fp4(WaveState<GQ> &W, unsigned char *st, 
 
     const u32x4 vm0 = *(const u32x4 *)(st + kMeta + 512 + 4 * (4 * r));
     const u32x4 vm1 = *(const u32x4 *)(st + kMeta + 512 + 4 * (64 + 4 * r));
+    // head q's score: rows 4q (rounded product) + 4q + 1 (residual), times
+    // sm_scale log2(e) 2^24 / 4^a
     float sv[2][4];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
         for (int a = 0; a < 4; ++a)
-            sv[cb][a] = S[cb][a][0] * (1.0f / (float)(1 << (2 * a)));
+            sv[cb][a] = (S[cb][a][0] + S[cb][a][1]) * (W.qk_c * (kSub / (float)(1 << (2 * a))));
     float mx = sv[0][0];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
         for (int a = 0; a < 4; ++a)
             mx = fmaxf(mx, sv[cb][a]);
-    const float yk = Yt[0];
+    const float yk = (Yt[0] + Yt[1]) * W.qk_c;
     mx = row_max16(mx) - yk;
     const float mn = fmaxf(W.m_run[0], mx);
     const float alpha = __builtin_amdgcn_exp2f(W.m_run[0] - mn);
@@ -511,12 +518,6 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     constexpr int HPL = GQ / 4;
     constexpr int RSTEP = 4 / HPL;  // accumulator register of head slot j = j * RSTEP
     const int q = lane >> 4, r = lane & 15;
-    // materialised per page (4 moves): held across the page loop it is spilled
-    u32x4 n1024 = {0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u};
-    asm volatile("" : "+v"(n1024));
-    const half8 neg1024 = __builtin_bit_cast(half8, n1024);
-
-    const CodeMasks &cm = W.cm;
 
     // ---------------- operands from LDS, issued together
     u32x4 ks[4], kz[4];
@@ -540,31 +541,47 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
             ksh[i] = *(const _Float16 *)(st + kMeta + 2 * W.hch[i]);
     }
 
-    // ---------------- QK A operands and the bias tiles X = -1024 sum A,
-    // Y = sum A z (per head row, broadcast over token columns)
-    half8 A[4], Ahi;
-    f32x4 Xt = {0.0f, 0.0f, 0.0f, 0.0f}, Yt = {0.0f, 0.0f, 0.0f, 0.0f};
+    // ---------------- QK A operands q s_k (rounded product and residual
+    // rows, qk_residual; GQA 16: residual operands Al for a second chain)
+    // and the bias tile Y = sum A z (per head row, broadcast over token
+    // columns)
+    half8 A[4], Ahi, Al[4], Alhi;
+    f32x4 Yt = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         u32x4 av;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             av[j] = as_u(as_h2(W.qv[s][j]) * as_h2(ks[s][j]));
+        if constexpr (GQ == 16) {
+            u32x4 lo = av;
+            qk_residual(lo, W.qv[s], ks[s], ~0ull);
+            Al[s] = __builtin_bit_cast(half8, lo);
+            Yt = mfma(Al[s], __builtin_bit_cast(half8, kz[s]), Yt);
+        } else {
+            qk_residual(av, W.qv[s], ks[s], kResidualLanes<GQ>);
+        }
         A[s] = __builtin_bit_cast(half8, av);
-        Xt = mfma(A[s], neg1024, Xt);
         Yt = mfma(A[s], __builtin_bit_cast(half8, kz[s]), Yt);
     }
     if (Dk > 0) {
-        u32x4 av;
+        u32x4 av, sh;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             half2v h;
             h[0] = ksh[2 * j];
             h[1] = ksh[2 * j + 1];
+            sh[j] = as_u(h);
             av[j] = as_u(as_h2(W.qvh[j]) * h);
         }
+        if constexpr (GQ == 16) {
+            u32x4 lo = av;
+            qk_residual(lo, W.qvh, sh, ~0ull);
+            Alhi = __builtin_bit_cast(half8, lo);
+        } else {
+            qk_residual(av, W.qvh, sh, kResidualLanes<GQ>);
+        }
         Ahi = __builtin_bit_cast(half8, av);
-        Xt = mfma(Ahi, neg1024, Xt);
     }
 
     // The MFMA blocks run at raised wave priority: the other wave of the SIMD
@@ -572,30 +589,36 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     // stays fed (measured: 1.5-2 us less per launch at config 3).
     __builtin_amdgcn_s_setprio(1);
     // ---------------- QK token tiles: S[cb][a] covers tokens 64cb + 4r + a.
-    // Every chain starts from X, so S[cb][a] ends at 4^a sum_k A c; the
-    // softmax subtracts the zero-point term Y.
+    // S[cb][a] ends at 4^a 2^-24 sum_k A c; the softmax scales it back and
+    // subtracts the zero-point term Y.
     f32x4 S[2][4];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
-        S[0][a] = S[1][a] = Xt;
+        S[0][a] = S[1][a] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
             const RawCodes rc = raw_codes(kraw[s][cb]);
-            S[cb][0] = mfma(A[s], codes_to_half8<0>(rc, cm), S[cb][0]);
-            S[cb][1] = mfma(A[s], codes_to_half8<1>(rc, cm), S[cb][1]);
-            S[cb][2] = mfma(A[s], codes_to_half8<2>(rc, cm), S[cb][2]);
-            S[cb][3] = mfma(A[s], codes_to_half8<3>(rc, cm), S[cb][3]);
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const half8 kc = slot_codes(rc, a);
+                S[cb][a] = mfma(A[s], kc, S[cb][a]);
+                if constexpr (GQ == 16)
+                    S[cb][a] = mfma(Al[s], kc, S[cb][a]);
+            }
         }
     if (Dk > 0) {
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
             const RawCodes rc = raw_codes(hraw[cb]);
-            S[cb][0] = mfma(Ahi, codes_to_half8<0>(rc, cm), S[cb][0]);
-            S[cb][1] = mfma(Ahi, codes_to_half8<1>(rc, cm), S[cb][1]);
-            S[cb][2] = mfma(Ahi, codes_to_half8<2>(rc, cm), S[cb][2]);
-            S[cb][3] = mfma(Ahi, codes_to_half8<3>(rc, cm), S[cb][3]);
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const half8 kc = slot_codes(rc, a);
+                S[cb][a] = mfma(Ahi, kc, S[cb][a]);
+                if constexpr (GQ == 16)
+                    S[cb][a] = mfma(Alhi, kc, S[cb][a]);
+            }
         }
     }
 
@@ -617,17 +640,19 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     _Float16 *pbuf = (_Float16 *)(st + kKlo);
     const u32x4 vm0 = *(const u32x4 *)(st + kMeta + 512 + 4 * (4 * r));
     const u32x4 vm1 = *(const u32x4 *)(st + kMeta + 512 + 4 * (64 + 4 * r));
-    const half2v ones = as_h2(0x3C003C00u);
-    float alpha[HPL], xv[HPL], yv[HPL];
+    float alpha[HPL], yv[HPL];
 #pragma unroll
     for (int j = 0; j < HPL; ++j) {
         const int ri = j * RSTEP;
+        // the head's score: its rounded-product row plus (GQA 8) its residual
+        // row, times sm_scale log2(e) 2^24 / 4^a
         float sv[2][4];
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
             for (int a = 0; a < 4; ++a)
-                sv[cb][a] = S[cb][a][ri] * (1.0f / (float)(1 << (2 * a)));
+                sv[cb][a] = (GQ == 16 ? S[cb][a][ri] : S[cb][a][ri] + S[cb][a][ri + 1]) *
+                            (W.qk_c * (kSub / (float)(1 << (2 * a))));
         float mx = sv[0][0];
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb)
@@ -635,13 +660,13 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
             for (int a = 0; a < 4; ++a)
                 mx = fmaxf(mx, sv[cb][a]);
         // scores are sv - Y: the max over the row and the exponents absorb Y
-        const float yk = Yt[ri];
+        const float yk = (GQ == 16 ? Yt[ri] : Yt[ri] + Yt[ri + 1]) * W.qk_c;
         mx = row_max16(mx) - yk;
         const float mn = fmaxf(W.m_run[j], mx);
         alpha[j] = __builtin_amdgcn_exp2f(W.m_run[j] - mn);
         W.m_run[j] = mn;
         const float mny = mn + yk;
-        float lsum = 0.0f, xsum = 0.0f, ysum = 0.0f;
+        float lsum = 0.0f, ysum = 0.0f;
         const int h = q * HPL + j;
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
@@ -658,18 +683,16 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
             const half2v zv23 = as_h2(__builtin_amdgcn_perm(vm[3], vm[2], 0x07060302u));
             const half2v a01 = as_h2(pack_h2(p0v, p1v)) * sv01;
             const half2v a23 = as_h2(pack_h2(p2v, p3v)) * sv23;
-            xsum = __builtin_amdgcn_fdot2(a01, ones, xsum, false);
-            xsum = __builtin_amdgcn_fdot2(a23, ones, xsum, false);
             ysum = __builtin_amdgcn_fdot2(a01, zv01, ysum, false);
             ysum = __builtin_amdgcn_fdot2(a23, zv23, ysum, false);
             *(uint2 *)(pbuf + h * 128 + 64 * cb + 4 * r) = make_uint2(as_u(a01), as_u(a23));
         }
         W.l_run[j] = W.l_run[j] * alpha[j] + lsum;
-        xv[j] = 1024.0f * row_sum16(xsum);
         yv[j] = row_sum16(ysum);
     }
 
-    // ---------------- PV: O_a = O_a * alpha - (1024 sum P' + 4^a sum P' z) + P' V
+    // ---------------- PV, in the subnormal codes' units 4^a 2^-24:
+    // O_a = O_a * alpha - 4^a 2^-24 sum P' z + P' C_a
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
@@ -677,7 +700,7 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
 #pragma unroll
             for (int j = 0; j < HPL; ++j)
                 W.O[cb][a][j * RSTEP] =
-                    W.O[cb][a][j * RSTEP] * alpha[j] - (xv[j] + yv[j] * (float)(1 << (2 * a)));
+                    W.O[cb][a][j * RSTEP] * alpha[j] - yv[j] * ((float)(1 << (2 * a)) / kSub);
     // P' rows are read with inline asm: the compiler cannot tell this stage
     // apart from the one the next page is streaming into and would otherwise
     // wait for that prefetch (vmcnt(0)) here.  LDS executes a wave's
@@ -701,10 +724,10 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
             const RawCodes rc = raw_codes(vraw[s][cb]);
-            W.O[cb][0] = mfma(Ap[s], codes_to_half8<0>(rc, cm), W.O[cb][0]);
-            W.O[cb][1] = mfma(Ap[s], codes_to_half8<1>(rc, cm), W.O[cb][1]);
-            W.O[cb][2] = mfma(Ap[s], codes_to_half8<2>(rc, cm), W.O[cb][2]);
-            W.O[cb][3] = mfma(Ap[s], codes_to_half8<3>(rc, cm), W.O[cb][3]);
+            W.O[cb][0] = mfma(Ap[s], codes_to_half8<0>(rc), W.O[cb][0]);
+            W.O[cb][1] = mfma(Ap[s], codes_to_half8<1>(rc), W.O[cb][1]);
+            W.O[cb][2] = mfma(Ap[s], codes_to_half8<2>(rc), W.O[cb][2]);
+            W.O[cb][3] = mfma(Ap[s], codes_to_half8<3>(rc), W.O[cb][3]);
         }
     __builtin_amdgcn_s_setprio(0);
 }
@@ -789,11 +812,13 @@ __device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned cha
     __syncthreads();
 
     WaveState<GQ> W;
-    W.cm = code_masks();
-    // Static halves of the QK A operand: q * sm_scale * log2(e) / 2^e for the
-    // lane's 8 channels of every K-step; zero on rows that carry no head.
+    // Static half of the QK A operand: the fp16 q of the lane's 8 channels
+    // of every K-step on the two rows of each head (the product with the key
+    // scale and its residual, qk_residual), zero on the other rows.
+    // sm_scale * log2(e) scales the scores, so A stays exact.
     W.prow = hr;
-    const float qscale = head_row ? p.sm_scale * kLog2e : 0.0f;
+    W.qk_c = p.sm_scale * kLog2e;
+    const bool qk_row = GQ == 16 || (r % ROWS_PER_HEAD) < 2;
     {
         const u32x4 *qraw = su.qraw;
 #pragma unroll
@@ -807,13 +832,11 @@ __device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned cha
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const half2v h = as_h2(qraw[s][j]);
-                W.qv[s][j] = pack_h2((float)h[0] * qscale, (float)h[1] * qscale);
-            }
+            for (int j = 0; j < 4; ++j)
+                W.qv[s][j] = qk_row ? qraw[s][j] : 0u;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float inv = qscale * 4.0f;  // high bits weigh 4
+            const float inv = qk_row ? 4.0f : 0.0f;  // high bits weigh 4 (exact in fp16)
             const int r0 = 8 * q + 2 * j;
             W.qvh[j] = pack_h2(r0 < Dk ? (float)qh[2 * j] * inv : 0.0f,
                                r0 + 1 < Dk ? (float)qh[2 * j + 1] * inv : 0.0f);
@@ -941,9 +964,10 @@ __device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned cha
         } else {
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb) {
-                // output tile a holds 4^a O for channels 64cb + 4r + a
-                float4 v = make_float4(W.O[cb][0][j * RSTEP], W.O[cb][1][j * RSTEP] * 0.25f,
-                                       W.O[cb][2][j * RSTEP] * 0.0625f, W.O[cb][3][j * RSTEP] * 0.015625f);
+                // output tile a holds 4^a 2^-24 O for channels 64cb + 4r + a
+                float4 v = make_float4(W.O[cb][0][j * RSTEP] * kSub, W.O[cb][1][j * RSTEP] * (kSub * 0.25f),
+                                       W.O[cb][2][j * RSTEP] * (kSub * 0.0625f),
+                                       W.O[cb][3][j * RSTEP] * (kSub * 0.015625f));
                 if (poison)
                     v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
                 *(float4 *)(o + 64 * cb + 4 * r) = v;

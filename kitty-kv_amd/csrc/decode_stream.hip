@@ -30,6 +30,7 @@
 // the page loop.
 #include "common.h"
 #include "decode.h"
+#include "qk_exact.h"
 
 namespace kitty {
 namespace stream {
@@ -300,8 +301,9 @@ __device__ __forceinline__ void issue_page(lds_t *st, const PageSrc &s, uint32_t
 template <int GQ>
 struct Seg {
     static constexpr int HPL = GQ / 4;  // heads per lane group
-    u32x4 qv[4];                        // q' fp16 pairs: the lane's 8 channels of each 32-channel K-step
-    u32x4 qvh;                          // 4 q'[channel(rank)] of high-bit rows 8q .. 8q + 7
+    u32x4 qv[4];                        // fp16 q pairs: the lane's 8 channels of each 32-channel K-step
+    u32x4 qvh;                          // 4 q[channel(rank)] of high-bit rows 8q .. 8q + 7
+    float qk_c;                         // sm_scale * log2(e): scores in log2 units
     unsigned hch2[2];                   // channel(rank 8q + i) in byte i of the pair (bytes 0-3, 4-7)
     int trk0;                           // tr8 offset (key regions), byte columns 0-15 (16-31: trk0 ^ 16)
     int trv0;                           // tr4 offset of value rows 32q + r, 16-byte chunk 0 (chunk 1: trv0 ^ 16)
@@ -319,7 +321,7 @@ __device__ __forceinline__ void page_qk(const Seg<GQ> &W, const lds_t *st, int l
     constexpr int HPL = GQ / 4;
     constexpr int RSTEP = 4 / HPL;  // accumulator register of head slot j
     const int q = lane >> 4;
-    half8 Ahi;
+    half8 Ahi, Alhi;
     if (Dk > 0) {
         // key scales of the boosted channels: channel(rank 8q + i) is byte i
         // of hch2 (the asm keeps the unpacking in the loop: hoisted, the eight
@@ -327,13 +329,21 @@ __device__ __forceinline__ void page_qk(const Seg<GQ> &W, const lds_t *st, int l
         unsigned h0 = W.hch2[0], h1 = W.hch2[1];
         asm volatile("" : "+v"(h0), "+v"(h1));
         const unsigned hc[2] = {h0, h1};
-        u32x4 av;
+        u32x4 av, sh;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             half2v h;
             h[0] = ldsr<_Float16>(st, kMeta + 2 * __builtin_amdgcn_ubfe(hc[j >> 1], 16 * (j & 1), 8));
             h[1] = ldsr<_Float16>(st, kMeta + 2 * __builtin_amdgcn_ubfe(hc[j >> 1], 16 * (j & 1) + 8, 8));
+            sh[j] = as_u(h);
             av[j] = as_u(as_h2(W.qvh[j]) * h);
+        }
+        if constexpr (GQ == 16) {
+            u32x4 lo = av;
+            qk_residual(lo, W.qvh, sh, ~0ull);
+            Alhi = __builtin_bit_cast(half8, lo);
+        } else {
+            qk_residual(av, W.qvh, sh, kResidualLanes<GQ>);
         }
         Ahi = __builtin_bit_cast(half8, av);
     }
@@ -347,40 +357,63 @@ __device__ __forceinline__ void page_qk(const Seg<GQ> &W, const lds_t *st, int l
             S[a] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            // A = q' * scale_k, rebuilt per half: four registers live instead of sixteen
+            // A = q * scale_k (rounded product and residual rows, qk_residual;
+            // GQA 16: residual operand Al for a second chain), rebuilt per
+            // half: four registers live instead of sixteen
             const u32x4 ks = ldsr<u32x4>(st, kMeta + 2 * (32 * s + 8 * q));
             u32x4 av;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 av[j] = as_u(as_h2(W.qv[s][j]) * as_h2(ks[j]));
+            half8 Al;
+            if constexpr (GQ == 16) {
+                u32x4 lo = av;
+                qk_residual(lo, W.qv[s], ks, ~0ull);
+                Al = __builtin_bit_cast(half8, lo);
+            } else {
+                qk_residual(av, W.qv[s], ks, kResidualLanes<GQ>);
+            }
             const half8 A = __builtin_bit_cast(half8, av);
             if (cb == 0) {
-                const u32x4 kz = ldsr<u32x4>(st, kMeta + 256 + 2 * (32 * s + 8 * q));
-                Yt = mfma(A, __builtin_bit_cast(half8, kz), Yt);
+                const half8 kz = __builtin_bit_cast(half8, ldsr<u32x4>(st, kMeta + 256 + 2 * (32 * s + 8 * q)));
+                Yt = mfma(A, kz, Yt);
+                if constexpr (GQ == 16)
+                    Yt = mfma(Al, kz, Yt);
             }
             const RawCodes rc = raw_codes(tr8(st, kKlo + 1024 * s + tb));
-            S[0] = mfma(A, sub_codes<0>(rc), S[0]);
-            S[1] = mfma(A, sub_codes<1>(rc), S[1]);
-            S[2] = mfma(A, sub_codes<2>(rc), S[2]);
-            S[3] = mfma(A, sub_codes<3>(rc), S[3]);
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const half8 kc = a == 0 ? sub_codes<0>(rc) : a == 1 ? sub_codes<1>(rc) : a == 2 ? sub_codes<2>(rc)
+                                                                                                 : sub_codes<3>(rc);
+                S[a] = mfma(A, kc, S[a]);
+                if constexpr (GQ == 16)
+                    S[a] = mfma(Al, kc, S[a]);
+            }
         }
         if (Dk > 0) {
             const RawCodes rc = raw_codes(tr8(st, kKhi + tb));
-            S[0] = mfma(Ahi, sub_codes<0>(rc), S[0]);
-            S[1] = mfma(Ahi, sub_codes<1>(rc), S[1]);
-            S[2] = mfma(Ahi, sub_codes<2>(rc), S[2]);
-            S[3] = mfma(Ahi, sub_codes<3>(rc), S[3]);
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const half8 kc = a == 0 ? sub_codes<0>(rc) : a == 1 ? sub_codes<1>(rc) : a == 2 ? sub_codes<2>(rc)
+                                                                                                 : sub_codes<3>(rc);
+                S[a] = mfma(Ahi, kc, S[a]);
+                if constexpr (GQ == 16)
+                    S[a] = mfma(Alhi, kc, S[a]);
+            }
         }
+        // a head's score: its rounded-product row plus (GQA 4 / 8) its
+        // residual row, times sm_scale log2(e)
         if (cb == 0) {
 #pragma unroll
             for (int j = 0; j < HPL; ++j)
-                y[j] = Yt[j * RSTEP];
+                y[j] = (GQ == 16 ? Yt[j * RSTEP] : Yt[j * RSTEP] + Yt[j * RSTEP + 1]) * W.qk_c;
         }
 #pragma unroll
         for (int j = 0; j < HPL; ++j)
 #pragma unroll
             for (int a = 0; a < 4; ++a)
-                sc[j][cb][a] = S[a][j * RSTEP] * (kSub / (float)(1 << (2 * a)));
+                sc[j][cb][a] = (GQ == 16 ? S[a][j * RSTEP] : S[a][j * RSTEP] + S[a][j * RSTEP + 1]) *
+                               (W.qk_c * (kSub / (float)(1 << (2 * a))));
     }
     __builtin_amdgcn_sched_barrier(0);
 }
@@ -608,7 +641,9 @@ __device__ __forceinline__ void seg_init(Seg<GQ> &W, const DecodeParams &p, cons
     }
     __syncthreads();
     W.prow = hr;
-    const float qscale = head_row ? p.sm_scale * kLog2e : 0.0f;
+    W.qk_c = p.sm_scale * kLog2e;
+    // the fp16 q on the two rows of each head (qk_residual), zero elsewhere
+    const bool qk_row = GQ == 16 || (r % ROWS_PER_HEAD) < 2;
     _Float16 qh[8];
     W.hch2[0] = W.hch2[1] = 0;
 #pragma unroll
@@ -620,13 +655,11 @@ __device__ __forceinline__ void seg_init(Seg<GQ> &W, const DecodeParams &p, cons
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const half2v h = as_h2(su.qraw[s][j]);
-            W.qv[s][j] = pack_h2((float)h[0] * qscale, (float)h[1] * qscale);
-        }
+        for (int j = 0; j < 4; ++j)
+            W.qv[s][j] = qk_row ? su.qraw[s][j] : 0u;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const float inv = qscale * 4.0f;  // high bits weigh 4
+        const float inv = qk_row ? 4.0f : 0.0f;  // high bits weigh 4 (exact in fp16)
         const int r0 = 8 * q + 2 * j;
         W.qvh[j] = pack_h2(r0 < Dk ? (float)qh[2 * j] * inv : 0.0f, r0 + 1 < Dk ? (float)qh[2 * j + 1] * inv : 0.0f);
     }
@@ -760,22 +793,20 @@ struct Fp16State {
 };
 
 // A operand of the FP16 QK: row r = head r (rows past GQ are zero), k = 8 kq
-// + i of each 32-channel step, q * sm_scale * log2(e) in fp16.
+// + i of each 32-channel step, the fp16 q as is (q k is exact in the fp32
+// accumulator; fp16_step scales the scores by sm_scale log2(e)).
 template <int GQ>
 __device__ __forceinline__ void fp16_qa(const DecodeParams &p, int b, int kh, half8 (&qa)[4])
 {
     const int lane = threadIdx.x, r = lane & 15, kq = lane >> 4;
-    const float qscale = p.sm_scale * kLog2e;
     const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + (r < GQ ? r : 0)) * p.q_s_head;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         const u32x4 raw = *(const u32x4 *)(qrow + 32 * s + 8 * kq);
         u32x4 v;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const half2v h = as_h2(raw[j]);
-            v[j] = r < GQ ? pack_h2((float)h[0] * qscale, (float)h[1] * qscale) : 0u;
-        }
+        for (int j = 0; j < 4; ++j)
+            v[j] = r < GQ ? raw[j] : 0u;
         qa[s] = __builtin_bit_cast(half8, v);
     }
 }
@@ -794,8 +825,8 @@ __device__ __forceinline__ float fp16_rescale(float &m, float mx)
 // repeat the last).  K chunk c of token row n is stored at chunk c ^ n so the
 // 16 rows one MFMA B read touches hit 16 bank groups.
 template <int GQ, typename KR, typename VR>
-__device__ __forceinline__ void fp16_step(Fp16State<GQ> &F, const half8 (&qa)[4], lds_t *st, int cnt, KR krow,
-                                          VR vrow)
+__device__ __forceinline__ void fp16_step(Fp16State<GQ> &F, const half8 (&qa)[4], float qk_c, lds_t *st, int cnt,
+                                          KR krow, VR vrow)
 {
     const int lane = threadIdx.x, r = lane & 15, kq = lane >> 4;
     constexpr int kP = 8192;  // P: fp32 [head][16]
@@ -812,6 +843,9 @@ __device__ __forceinline__ void fp16_step(Fp16State<GQ> &F, const half8 (&qa)[4]
 #pragma unroll
     for (int s = 0; s < 4; ++s)
         S = mfma(qa[s], ldsr<half8>(st, 256 * r + 16 * ((4 * s + kq) ^ r)), S);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        S[i] *= qk_c;
     float alpha[GQ];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -988,7 +1022,7 @@ __device__ __attribute__((noinline)) void fp16_region(KernargParams kp, int b, i
         fp16_qa<GQ>(P, b, kh, qa);
         const int s1 = min(hi, L.ns);
         for (int c0 = lo; c0 < s1; c0 += 16)
-            fp16_step<GQ>(F, qa, st, min(16, s1 - c0), [&](int n) { return sk + (c0 + n) * sks; },
+            fp16_step<GQ>(F, qa, P.sm_scale * kLog2e, st, min(16, s1 - c0), [&](int n) { return sk + (c0 + n) * sks; },
                           [&](int n) { return sv + (c0 + n) * svs; });
     }
     // key pages npv .. npk - 1: QK from the page, values from the value tail
@@ -1013,7 +1047,7 @@ __device__ __attribute__((noinline)) void fp16_region(KernargParams kp, int b, i
         fp16_qa<GQ>(P, b, kh, qa);
         for (int c0 = max(lo, L.ns + L.nmix); c0 < hi; c0 += 16) {
             const int u = c0 - L.ns - L.nmix;  // key tail row
-            fp16_step<GQ>(F, qa, st, min(16, hi - c0), [&](int n) { return tk + (u + n) * tks; },
+            fp16_step<GQ>(F, qa, P.sm_scale * kLog2e, st, min(16, hi - c0), [&](int n) { return tk + (u + n) * tks; },
                           [&](int n) { return tv + (L.nmix + u + n) * tvs; });
         }
     }

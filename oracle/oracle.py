@@ -19,6 +19,10 @@ Parity pins (tests/test_oracle.py): the reference's two known-answer tests
 (``:56-113``, ``:206-230``), hand-derived tie and underflow cases, brute force
 over every 4-token code pattern at G=4, and the paged attention checked against
 torch's ``scaled_dot_product_attention`` on the oracle's dequantised K/V.
+``paged_attention_kv`` (independent key and value streams) is pinned by its
+reduction to the C paged attention when both streams hold the same pages, by
+the equivalence of a value page and its dequantised rows in the FP16 value
+tail, and by SDPA on the assembled streams.
 Only the sign of a zero zero-point and the reference's fp32 summation order
 are unpinned; both are compared by value / within tolerance.
 """
@@ -268,3 +272,47 @@ def dequantized_kv(page_list, key_baseline, key_boost, key_meta, value_pool, val
         Ks.append(np.concatenate(kp, 0) if kp else np.zeros((0, D), np.float32))
         Vs.append(np.concatenate(vp_, 0) if vp_ else np.zeros((0, D), np.float32))
     return Ks, Vs
+
+
+# ------------------------------------- independent key and value streams
+
+def split_stream_kv(key_pages, value_pages, key_baseline, key_boost, key_meta, value_pool, value_meta,
+                    boost_idx, d_boost, sink_k, sink_v, tail_k, tail_v):
+    """Per KV head, the key stream sinks | key_pages | tail_k and the value
+    stream sinks | value_pages | tail_v as fp32 (T, D) arrays: the layout a
+    value local window gives (KIVI: keys are quantised a page at a time,
+    values once they leave the last R tokens), where the most recent tokens
+    of the key stream's pages may still be FP16 values.  The two streams
+    must have the same length.  With value_pages == key_pages and equal
+    tails this is what paged_attention_reference attends to
+    (kitty/kernels/attention.py:136-168; the window's spill rule is
+    kitty/pipeline.py:155-168)."""
+    Ks, _ = dequantized_kv(key_pages, key_baseline, key_boost, key_meta, value_pool, value_meta,
+                           boost_idx, d_boost, sink_k, sink_v, tail_k, tail_k)
+    _, Vs = dequantized_kv(value_pages, key_baseline, key_boost, key_meta, value_pool, value_meta,
+                           boost_idx, d_boost, sink_v, sink_v, tail_v, tail_v)
+    for K, V in zip(Ks, Vs):
+        if K.shape != V.shape:
+            raise ValueError(f"key stream has {K.shape[0]} tokens, value stream {V.shape[0]}")
+    return Ks, Vs
+
+
+def paged_attention_kv(q, key_pages, value_pages, key_baseline, key_boost, key_meta, value_pool, value_meta,
+                       boost_idx, d_boost: int, sink_k, sink_v, tail_k, tail_v, num_q_heads: int,
+                       num_kv_heads: int, head_dim: int) -> np.ndarray:
+    """(Hq, D) fp16 decode output over independent key and value streams
+    (split_stream_kv): softmax(q K^T / sqrt(D)) V per query head, KV head
+    qh // (Hq / H), in float64; zeros for an empty context."""
+    Ks, Vs = split_stream_kv(key_pages, value_pages, key_baseline, key_boost, key_meta, value_pool, value_meta,
+                             boost_idx, d_boost, sink_k, sink_v, tail_k, tail_v)
+    g = num_q_heads // num_kv_heads
+    out = np.zeros((num_q_heads, head_dim), np.float64)
+    qd = np.asarray(q, np.float16).astype(np.float64)
+    for qh in range(num_q_heads):
+        K, V = Ks[qh // g].astype(np.float64), Vs[qh // g].astype(np.float64)
+        if K.shape[0] == 0:
+            continue
+        s = K @ qd[qh] / np.sqrt(head_dim)
+        p = np.exp(s - s.max())
+        out[qh] = (p / p.sum()) @ V
+    return out.astype(np.float16)

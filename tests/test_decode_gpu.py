@@ -273,3 +273,63 @@ def test_config4_ragged_batch_64bit_offsets(dev):
         ref = O.paged_attention(q[b].numpy(), bt_compact[b, :n].numpy(), kb, kh, km, vp, vm, bi.numpy(), dk,
                                 sk[b].numpy(), sv[b].numpy(), tk[b, :, :t].numpy(), tv[b, :, :t].numpy(), Hq, H, D)
         _close(out[b], ref, f"config4 b={b} ctx={ctx[b]}")
+
+
+@pytest.mark.parametrize("kernel,Hq,H,D,G,dk", [("stream", 32, 8, 128, 128, 16), ("stream", 64, 8, 128, 128, 32),
+                                               ("generic", 8, 4, 64, 32, 8)])
+def test_independent_value_stream(dev, kernel, Hq, H, D, G, dk):
+    """Key and value streams of different page counts (P_v <= P_k, the value
+    local window of the pipeline): the value rows of key pages P_v..P_k-1 and
+    of the key tail come from tail_v, (P_k - P_v) G + tail_len rows of it.
+    Against the oracle's split-stream decode, per sequence and head, with
+    P_v = P_k (the reference layout), P_v = P_k - 1 (a 128-token window),
+    P_v = 0 (every value FP16) and P_v = P_k - 2."""
+    from kitty.kernels import paged_attention_batched
+    S = 32 if D == 128 else 40
+    ctx = [S + 6 * G + 17, S + 3 * G, S + 2 * G + G - 1, S + 1 * G + 5, S + 9 * G + 60]
+    B = len(ctx)
+    c = _batched_case(dev, 90 + Hq, B, Hq, H, D, G, dk, ctx, S=S)
+    npk = c["n_pages"]
+    npv = [npk[0], npk[1] - 1, 0, npk[3] - 1, npk[4] - 2]
+    nv = [(a - b) * G + t for a, b, t in zip(npk, npv, c["tails"])]
+    gen = torch.Generator().manual_seed(7)
+    tv = torch.randn(B, H, max(nv), D, generator=gen).half()
+    kb, kh, km, vp, vm = [t.to(dev) for t in c["pools"]]
+    i32 = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)
+    print(f"value stream {kernel} Hq={Hq}: npk={npk} npv={npv} nv={nv}", flush=True)
+    out = paged_attention_batched(
+        c["q"].to(dev), c["bt"].to(dev), i32(npk), kb, kh, km, vp, vm, c["bi"].to(dev), c["sk"].to(dev),
+        c["sv"].to(dev), i32([S] * B), c["tk"].to(dev), tv.to(dev), i32(c["tails"]),
+        num_pages_v=i32(npv), tail_len_v=i32(nv)).cpu().numpy()
+    pools = [t.numpy() for t in c["pools"]]
+    for b in range(B):
+        bt = c["bt"][b].numpy()
+        ref = O.paged_attention_kv(c["q"][b].numpy(), bt[:npk[b]], bt[:npv[b]], *pools, c["bi"].numpy(), dk,
+                                   c["sk"][b].numpy(), c["sv"][b].numpy(), c["tk"][b, :, :c["tails"][b]].numpy(),
+                                   tv[b, :, :nv[b]].numpy(), Hq, H, D)
+        _close(out[b], ref, f"{kernel} b={b} npk={npk[b]} npv={npv[b]}")
+
+
+def test_value_stream_length_mismatch_poisons_sequence(dev):
+    """A sequence whose value stream is not as long as its key stream
+    ((P_k - P_v) G + tail_len != tail_len_v) gets NaN output; the others
+    are unaffected."""
+    from kitty.kernels import paged_attention_batched
+    B, Hq, H, D, G, dk = 2, 32, 8, 128, 128, 16
+    c = _batched_case(dev, 95, B, Hq, H, D, G, dk, [32 + 4 * 128 + 9, 32 + 3 * 128 + 2])
+    npk, tails = c["n_pages"], c["tails"]
+    npv = [npk[0] - 1, npk[1] - 1]
+    nv = [128 + tails[0], 128 + tails[1] - 1]            # sequence 1 one row short
+    tv = torch.randn(B, H, max(nv), D, generator=torch.Generator().manual_seed(3)).half()
+    i32 = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)
+    kb, kh, km, vp, vm = [t.to(dev) for t in c["pools"]]
+    out = paged_attention_batched(
+        c["q"].to(dev), c["bt"].to(dev), i32(npk), kb, kh, km, vp, vm, c["bi"].to(dev), c["sk"].to(dev),
+        c["sv"].to(dev), i32([32] * B), c["tk"].to(dev), tv.to(dev), i32(tails),
+        num_pages_v=i32(npv), tail_len_v=i32(nv)).cpu().numpy()
+    assert np.isnan(out[1]).all()
+    bt = c["bt"][0].numpy()
+    ref = O.paged_attention_kv(c["q"][0].numpy(), bt[:npk[0]], bt[:npv[0]], *[t.numpy() for t in c["pools"]],
+                               c["bi"].numpy(), dk, c["sk"][0].numpy(), c["sv"][0].numpy(),
+                               c["tk"][0, :, :tails[0]].numpy(), tv[0, :, :nv[0]].numpy(), Hq, H, D)
+    _close(out[0], ref, "b=0")

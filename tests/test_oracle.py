@@ -314,3 +314,45 @@ def test_torch_restatement_matches_c_oracle():
     empty = TR.paged_attention(t["q"], [], t["kb"], t["kh"], t["km"], t["vp"], t["vm"], t["bi"], dk,
                                t["sk"][:, :0], t["sv"][:, :0], t["tk"][:, :0], t["tv"][:, :0], Hq, H, D)
     assert (empty.float() == 0).all()
+
+
+@pytest.mark.parametrize("npk,npv,nk", [(4, 4, 5), (4, 2, 5), (3, 0, 0), (5, 3, 7)])
+def test_split_stream_oracle(npk, npv, nk):
+    """Independent key / value streams (a value local window): the first npv
+    of npk pages carry values; the value rows of the other pages, followed
+    by the nk key-tail tokens' values, are FP16 in tail_v.
+
+    * tail_v holding exactly the dequantised values of pages npv..npk-1
+      (already fp16-exact: the page is quantised from them, then its
+      dequantised fp32 rows are rounded to fp16) gives the C oracle's
+      all-pages output up to that rounding;
+    * npv == npk with equal tails is the C oracle's output itself;
+    * SDPA on the assembled streams gives the same output."""
+    rng = np.random.default_rng(31 + npk + npv)
+    H, Hq, D, G, dk = 2, 8, 32, 16, 6
+    c = make_paged_case(rng, H, Hq, D, G, dk, npk, 3, nk)
+    keys, vals = list(c["pages"]), list(c["pages"][:npv])
+    moved = np.zeros((H, (npk - npv) * G, D), np.float16)
+    for j, p in enumerate(c["pages"][npv:]):
+        for h in range(H):
+            moved[h, j * G:(j + 1) * G] = O.dequantize_value(c["vp"][p, h], c["vm"][p, h, :, 0],
+                                                             c["vm"][p, h, :, 1]).astype(np.float16)
+    tv = np.concatenate([moved, c["tv"]], 1)
+    args = (c["kb"], c["kh"], c["km"], c["vp"], c["vm"], c["bi"], dk, c["sk"], c["sv"])
+    got = O.paged_attention_kv(c["q"], keys, vals, *args, c["tk"], tv, Hq, H, D).astype(np.float32)
+    # every page's values from the pools: equal up to the fp16 rounding of the moved rows
+    ref_all = O.paged_attention(c["q"], c["pages"], c["kb"], c["kh"], c["km"], c["vp"], c["vm"], c["bi"], dk,
+                                c["sk"], c["sv"], c["tk"], c["tv"], Hq, H, D).astype(np.float32)
+    assert np.allclose(got, ref_all, atol=3e-3, rtol=1e-2)
+    same = O.paged_attention_kv(c["q"], keys, keys, *args, c["tk"], c["tv"], Hq, H, D).astype(np.float32)
+    assert np.allclose(same, ref_all, atol=1e-3, rtol=1e-3)
+    Ks, Vs = O.split_stream_kv(keys, vals, *args, c["tk"], tv)
+    assert Ks[0].shape[0] == 3 + npk * G + nk
+    for qh in range(Hq):
+        K = torch.from_numpy(Ks[qh // (Hq // H)]).double()
+        V = torch.from_numpy(Vs[qh // (Hq // H)]).double()
+        qv = torch.from_numpy(c["q"][qh].astype(np.float64))[None, None, None]
+        ref = torch.nn.functional.scaled_dot_product_attention(qv, K[None, None], V[None, None])[0, 0, 0]
+        assert np.allclose(got[qh], ref.numpy(), atol=2e-3, rtol=1e-2)
+    with pytest.raises(ValueError):
+        O.split_stream_kv(keys, vals, *args, c["tk"], c["tv"][:, :0] if npv < npk else c["tv"][:, :1])
