@@ -15,9 +15,10 @@ i.e. the split-K kernel (pages + FP16 segments) and the merge kernel.  After
 at least --warmup steps and --warmup-seconds of them (steady clock whatever
 --steps is), `value` is microseconds per layer-step over exactly --steps
 back-to-back steps (host clock; inputs resident in HBM).  The roofline entry
-is for the split-K kernel: a second pass of the same alternating steps
-records a HIP event on the launch stream around every launch, giving each
-kernel's mean duration in the regime `value` is measured in.
+is for the split-K kernel: bursts of back-to-back launches between two HIP
+events on the launch stream, right after `value` at the same settled clock
+(per-launch event pairs in the alternating step pattern are reported as
+upper bounds).
 
 `legs` repeats this for configs 4 and 5, each with its own roofline block;
 `quantize_pack` times config 2's batch quantize; `cpu_baseline` is the
@@ -352,13 +353,13 @@ def time_decode(torch, plans, steps: int, warm_steps: int, warm_s: float) -> dic
 
     Warm-up: at least warm_steps steps and warm_s seconds of them, so the GPU
     clock has settled whatever --steps is.  `value`: exactly `steps`
-    back-to-back steps between two HIP events and by the host clock.  The
-    split / merge breakdown comes from a second pass of the same alternating
-    steps (at least 200) with an event recorded on the launch stream before
-    each split, between split and merge, and after each merge: per-launch
-    durations in the regime `value` is measured in.  An event pair adds its
-    marker gap to the launch it brackets, so these are upper bounds of the
-    kernel times (the rocprofv3 trace gives the bare ones)."""
+    back-to-back steps between two HIP events and by the host clock.  Kernel
+    times, right after at the same settled clock: five bursts of at least 100
+    back-to-back launches of the split kernel, then of the merge kernel,
+    each burst between two HIP events on the launch stream (median burst,
+    mean per launch).  A last pass of alternating steps with an event
+    around every launch gives per-launch times in the exact step pattern;
+    each marker adds a few microseconds, so those are upper bounds."""
     n = len(plans)
     t_end = time.perf_counter() + warm_s
     i = 0
@@ -379,6 +380,19 @@ def time_decode(torch, plans, steps: int, warm_steps: int, warm_s: float) -> dic
     torch.cuda.synchronize()
     wall_us = (time.perf_counter() - t0) * 1e6 / steps
     event_us = e0.elapsed_time(e1) * 1e3 / steps
+
+    def burst(fn, k) -> float:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for i in range(k):
+            fn(plans[i % n])
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / k
+    kb = max(steps, 100)
+    kernel_us = statistics.median(burst(lambda p: p.run_splits(), kb) for _ in range(5))
+    merge_us = statistics.median(burst(lambda p: p.run_merge(), kb) for _ in range(5))
     m = max(steps, 200)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * m + 1)]
     torch.cuda.synchronize()
@@ -393,12 +407,12 @@ def time_decode(torch, plans, steps: int, warm_steps: int, warm_s: float) -> dic
     split = [ev[2 * i].elapsed_time(ev[2 * i + 1]) * 1e3 for i in range(m)]
     merge = [ev[2 * i + 1].elapsed_time(ev[2 * i + 2]) * 1e3 for i in range(m)]
     step_inst = ev[0].elapsed_time(ev[2 * m]) * 1e3 / m
-    kernel_us = sum(split) / m
-    merge_us = sum(merge) / m
-    assert kernel_us <= step_inst, (kernel_us, step_inst)
+    # the split kernel is part of every step: its time cannot exceed the step's
+    assert kernel_us <= event_us, (kernel_us, event_us)
     return dict(wall_us=wall_us, event_us=event_us, kernel_us=kernel_us, merge_us=merge_us,
-                kernel_median_us=statistics.median(split), merge_median_us=statistics.median(merge),
-                step_instrumented_us=step_inst, instrumented_steps=m, warm_steps=warm_done, warm_s=warm_s)
+                kernel_event_us=sum(split) / m, merge_event_us=sum(merge) / m,
+                step_instrumented_us=step_inst, instrumented_steps=m, burst_launches=kb, warm_steps=warm_done,
+                warm_s=warm_s)
 
 
 def decode_leg(torch, dev, name: str, copies: int, placement: str, steps: int, warm_steps: int,
@@ -411,7 +425,8 @@ def decode_leg(torch, dev, name: str, copies: int, placement: str, steps: int, w
     log(f"{name}: pool {w['P']} pages, {nb['packed'] / 1e6:.1f} MB packed KV per step")
     t = time_decode(torch, w["plans"], steps, warm_steps, warm_s)
     log(f"{name}: {t['wall_us']:.1f} us/step wall ({t['event_us']:.1f} by events); split kernel "
-        f"{t['kernel_us']:.1f} us, merge {t['merge_us']:.1f} us (instrumented step {t['step_instrumented_us']:.1f})")
+        f"{t['kernel_us']:.1f} us, merge {t['merge_us']:.1f} us (bursts); per-launch events "
+        f"{t['kernel_event_us']:.1f} / {t['merge_event_us']:.1f} us in a {t['step_instrumented_us']:.1f} us step")
     kernel_us = t["kernel_us"]
     achieved = nb["total"] / (kernel_us * 1e-6) / 1e9
     packed_gbps = nb["packed"] / (kernel_us * 1e-6) / 1e9
@@ -434,8 +449,9 @@ def decode_leg(torch, dev, name: str, copies: int, placement: str, steps: int, w
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": f"decode_mfma_kernel<{GQ}> (split-K phase of kitty_paged_decode)",
                      "kernel_us": round(kernel_us, 2), "merge_us": round(t["merge_us"], 2),
-                     "kernel_median_us": round(t["kernel_median_us"], 2),
-                     "merge_median_us": round(t["merge_median_us"], 2),
+                     "burst_launches": t["burst_launches"],
+                     "kernel_event_us": round(t["kernel_event_us"], 2),
+                     "merge_event_us": round(t["merge_event_us"], 2),
                      "step_instrumented_us": round(t["step_instrumented_us"], 2),
                      "instrumented_steps": t["instrumented_steps"], "warmup_steps": t["warm_steps"],
                      "warmup_s": t["warm_s"],

@@ -234,11 +234,16 @@ int kitty_paged_decode_noalloc(const kitty_decode_args *args, kitty_stream_t str
  * (kitty/pipeline.py:115-181) for B sequences in one launch: sequence b's
  * new key / value (H x D) goes to row sink_fill[slot] of its sink buffer
  * while sink_fill[slot] < sink_size, else to row buf_len[slot] of its key /
- * value buffer, and that counter is incremented on the device.  A sequence
- * whose buffer already holds buf_tokens tokens (the caller did not spill it
- * with kitty_quantize_kv_blocks) is left unchanged and overflow[b] is set to
- * 1.  Slots must be distinct within one call.  Buffers and key / value rows
- * must be 16-byte aligned, head_dim a multiple of 8. */
+ * value buffer, and that counter is incremented on the device.
+ * With val_len set, values have a buffer and counter of their own (the
+ * value local window, pipeline.py:155-168: values leave FP16 later than
+ * keys): the value goes to row val_len[slot] of val_buf (val_tokens rows)
+ * and val_len is incremented; buf_v is then unused.  A sequence whose key
+ * buffer already holds buf_tokens tokens, or whose value buffer holds
+ * val_tokens (the caller did not spill it with kitty_quantize_kv_blocks), is
+ * left unchanged and overflow[b] is set to 1.  Slots must be distinct within
+ * one call.  Buffers and key / value rows must be 16-byte aligned, head_dim
+ * a multiple of 8. */
 typedef struct {
     int64_t s_slot, s_head, s_tok; /* element strides; the channel stride is 1 */
 } kitty_slot_layout;
@@ -255,6 +260,11 @@ typedef struct {
     int32_t *buf_len;            /* (num_slots,) tokens in each key / value buffer */
     int32_t *overflow;           /* (B,) */
     int32_t batch, num_kv_heads, head_dim, sink_size, buf_tokens, num_slots;
+    /* optional value stream (NULL val_len: values share buf_len and buf_v) */
+    int32_t *val_len;            /* (num_slots,) tokens in each value buffer */
+    uint16_t *val_buf;           /* (num_slots, H, val_tokens, D) of this layer */
+    kitty_slot_layout val_layout;
+    int32_t val_tokens;
 } kitty_append_args;
 
 int kitty_append_tokens(const kitty_append_args *args, kitty_stream_t stream);

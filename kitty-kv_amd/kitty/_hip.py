@@ -96,6 +96,7 @@ class AppendArgs(ctypes.Structure):
         ("sink_fill", _vp), ("buf_len", _vp), ("overflow", _vp),
         ("batch", _i32), ("num_kv_heads", _i32), ("head_dim", _i32), ("sink_size", _i32), ("buf_tokens", _i32),
         ("num_slots", _i32),
+        ("val_len", _vp), ("val_buf", _vp), ("val_layout", SlotLayout), ("val_tokens", _i32),
     ]
 
 

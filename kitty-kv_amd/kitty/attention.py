@@ -6,9 +6,14 @@ asserts B == 1 (``:100``); here row b of a (B, ...) call belongs to sequence
 ``seq_id[b]`` (a sequence of ids) or ``seq_id + b`` (an int).
 
 Decode (T == 1): the new K/V of all B sequences go through the pipeline (one
-batch-quantize launch for every sequence whose buffer fills), then one fused
-split-K paged decode attends sinks, pages and the FP16 tail of every
-sequence at once.
+append launch, and a batch-quantize launch for the sequences whose key or
+value buffer fills), then one fused split-K paged decode attends sinks,
+pages and the FP16 key / value tails of every sequence at once.  The decode
+plan of a batch (its validated kernel arguments and workspace) is built once
+per (layer, slot range) and reused while a batch occupies the same
+contiguous range of pipeline slots: it reads lengths, block table and
+buffers from the pipeline's device state, so a step only rebinds q and the
+output.  No step waits for the GPU.
 
 Prefill (T > 1): the chunk goes into the pipeline in bulk (sinks and buffer
 rows copied, every complete page quantised straight from the chunk in one
@@ -46,6 +51,7 @@ class KittyPagedAttention(nn.Module):
         self.pipeline = pipeline
         self.scale = 1.0 / math.sqrt(config.head_dim)
         self._boost_unique = boost_rows_unique(pipeline.boost_idx_uint8[layer_id], config.d_boost)
+        self._plans: dict = {}   # tuple(slots) -> DecodePlan over the pipeline's device state
 
     def _seq_ids(self, B: int, seq_id: Union[int, Sequence[int]]) -> List[int]:
         if isinstance(seq_id, int):
@@ -65,16 +71,30 @@ class KittyPagedAttention(nn.Module):
             return self._decode_step(q, k, v, seq_ids)
         return self._prefill(q, k, v, seq_ids)
 
-    def _decode_step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids: List[int]) -> torch.Tensor:
-        self.pipeline.push_tokens(self.layer_id, k[:, :, 0], v[:, :, 0], seq_ids)
-        x = self.pipeline.decode_inputs(self.layer_id, seq_ids)
+    def _plan(self, qd: torch.Tensor, seq_ids: List[int]) -> DecodePlan:
+        key = tuple(self.pipeline.slot(s) for s in seq_ids)
+        plan = self._plans.get(key)
+        if plan is not None:
+            return plan
+        x = self.pipeline.decode_inputs(self.layer_id, seq_ids, full_width=True)
         lay = self.layout
-        qd = q[:, :, 0].to(torch.float16).contiguous()
         plan = DecodePlan(qd, x["block_table"], x["num_pages"], lay.key_baseline, lay.key_boost, lay.key_metadata,
                           lay.value_pool, lay.value_metadata, self.pipeline.boost_idx_uint8[self.layer_id],
                           x["sink_k"], x["sink_v"], x["sink_len"], x["tail_k"], x["tail_v"], x["tail_len"],
-                          max_pages=x["max_pages"], sm_scale=self.scale, boost_unique=self._boost_unique)
-        return plan.run().unsqueeze(2).to(q.dtype)
+                          max_pages=x["max_pages"], sm_scale=self.scale, boost_unique=self._boost_unique,
+                          num_pages_v=x["num_pages_v"], tail_len_v=x["tail_len_v"])
+        if x["contiguous"]:      # views of the pipeline's state: valid for every later step
+            if len(self._plans) >= 16:
+                self._plans.clear()
+            self._plans[key] = plan
+        return plan
+
+    def _decode_step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids: List[int]) -> torch.Tensor:
+        self.pipeline.push_tokens(self.layer_id, k[:, :, 0], v[:, :, 0], seq_ids)
+        qd = q[:, :, 0].to(torch.float16).contiguous()
+        plan = self._plan(qd, seq_ids)
+        out = torch.empty(qd.shape, dtype=torch.float16, device=qd.device)
+        return plan.run_with(qd, out).unsqueeze(2).to(q.dtype)
 
     def _prefill(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids: List[int]) -> torch.Tensor:
         self.pipeline.push_chunk(self.layer_id, k, v, seq_ids)

@@ -254,6 +254,20 @@ class DecodePlan:
         _hip.check(self._L.kitty_paged_decode(ctypes.byref(self.args), _hip.stream_ptr(self.device)))
         return self.out
 
+    def run_with(self, q: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        """The same decode with another query and output of the plan's
+        shapes and strides (a plan cached across decode steps: everything
+        else it reads is device state that the steps update in place)."""
+        for name, t, ref in (("q", q, self._keep[0]), ("out", out, self.out)):
+            _need(t.device == self.device and t.dtype == torch.float16 and t.shape == ref.shape
+                  and t.stride() == ref.stride(), f"{name} must match the plan's shape, strides and device")
+        self.args.q, self.args.out = q.data_ptr(), out.data_ptr()
+        try:
+            _hip.check(self._L.kitty_paged_decode(ctypes.byref(self.args), _hip.stream_ptr(self.device)))
+        finally:
+            self.args.q, self.args.out = self._keep[0].data_ptr(), self.out.data_ptr()
+        return out
+
     def run_splits(self) -> None:
         _hip.check(self._L.kitty_paged_decode_splits(ctypes.byref(self.args), _hip.stream_ptr(self.device)))
 

@@ -9,32 +9,43 @@ deliberate:
   own counters.  The reference keeps one shared set and advances counters only
   on layer 0 (``pipeline.py:90-111, 146-177``), so layers >= 1 and a second
   sequence overwrite each other.
-* A spill quantises the G buffered tokens of key AND value into the same page,
-  so page p holds K and V of the same tokens and the FP16 key and value tails
-  have equal length (the contract of ``paged_attention_reference``,
-  ``kernels/attention.py:163-165``).  The reference quantises the values
-  evicted from its R-window instead, which pairs keys of page p with values of
-  page p-1 and zeros in page 0.  ``val_local_len`` therefore reports the
-  length of the FP16 value tail (equal to ``key_qbuf_len``) and
-  ``val_qbuf_len`` is always 0.
+* Keys and values leave FP16 on their own schedules (the KIVI split the
+  reference's local value window aims at, ``pipeline.py:100-108, 155-168``):
+  the keys of G buffered tokens are quantised into a new page as soon as the
+  key buffer is full, the values of those same G tokens once they are older
+  than the R most recent tokens.  After n tokens past the sinks a sequence
+  holds P_k = n // G key pages, P_v = max(0, n - R) // G value pages (the
+  value half of the same physical pages) and n - P_v G FP16 values (R to
+  R + G - 1 of them once n >= R + G), so the R most recent values are always
+  FP16.  Page p holds K and V of the same tokens.  The reference instead
+  quantises, at each key spill, the values its window has evicted so far,
+  which pairs the keys of page p with values of earlier tokens and zeros in
+  page 0.  ``val_local_len`` reports the values in the R-window and
+  ``val_qbuf_len`` the older FP16 values not yet quantised.  R = 0 gives the
+  single-stream layout of ``paged_attention_reference`` (equal key and value
+  tails, ``kernels/attention.py:163-165``).
 
 On a ROCm device the hot path of a decode step is:
 
 * one ``kitty_append_tokens`` launch that writes the new token of every
-  sequence of the batch into its sink or key / value buffer and advances the
-  device-side counters (``lens``: sink fill, buffer length, page count per
-  (layer, slot));
-* for the sequences whose buffer became full, one ``kitty_quantize_kv_blocks``
-  launch that packs all of them into freshly allocated pages, plus the block
-  table and counter updates;
+  sequence of the batch into its sink, key and value buffers and advances the
+  device-side counters (``lens``: sink fill, key buffer length, key pages,
+  value pages, value buffer length per (layer, slot));
+* for the sequences whose key buffer became full, one key-only
+  ``kitty_quantize_kv_blocks`` launch into freshly allocated pages; for those
+  whose value buffer reached R + G rows, one value-only launch into the value
+  half of their oldest value-less page, then a device-side shift of the
+  remaining R values (R = 0: one launch for both);
 * the decode reads lengths, block table rows and FP16 segments straight from
   these device tensors.
 
 Host state mirrors the counters (every push adds exactly one token per
 sequence, so the host knows when a buffer fills without reading the device);
-nothing here waits for the GPU.  A prompt (T > 1 tokens) goes through
-``push_chunk``: sinks and buffer rows are copied in bulk and every complete
-G-token page of the chunk is quantised straight from the chunk in one launch.
+nothing here waits for the GPU: the few host-side integers a spill needs on
+the device (slots, page ids, page numbers) go through pinned memory with
+non-blocking copies on the current stream.  A prompt (T > 1 tokens) goes
+through ``push_chunk``: sinks and buffer rows are copied in bulk and every
+complete G-token page of the chunk is quantised straight from it.
 """
 from __future__ import annotations
 
@@ -49,7 +60,7 @@ from .config import KittyConfig
 from .layout import PageCentricKVLayoutManager
 from .kernels.ops import pool_store, quantize_into_pools
 
-_FILL, _QLEN, _NPAGES = 0, 1, 2
+_FILL, _QLEN, _NPAGES, _NPAGES_V, _VLEN = 0, 1, 2, 3, 4
 
 
 class KittyInferencePipeline:
@@ -63,23 +74,27 @@ class KittyInferencePipeline:
         self.device = dev
         self.boost_idx_uint8 = boost_idx_uint8.to(dev, torch.uint8).contiguous()  # (L, H, D)
         L, H, D = config.num_layers, config.num_kv_heads, config.head_dim
-        S, G = config.sink_size, config.q_buffer_size
+        S, G, R = config.sink_size, config.q_buffer_size, config.local_value_window
         self.num_slots = max(1, int(num_slots or config.max_batch_size))
+        self.value_capacity = R + G     # FP16 values a sequence can hold before its value spill
         n = self.num_slots
         f16 = torch.float16
         self._sink_k = torch.zeros(n, L, H, S, D, dtype=f16, device=dev)
         self._sink_v = torch.zeros(n, L, H, S, D, dtype=f16, device=dev)
         self._qbuf_k = torch.zeros(n, L, H, G, D, dtype=f16, device=dev)
-        self._qbuf_v = torch.zeros(n, L, H, G, D, dtype=f16, device=dev)
+        self._vbuf = torch.zeros(n, L, H, self.value_capacity, D, dtype=f16, device=dev)
         # host mirrors of the counters, (slot, layer)
         self._fill = np.zeros((n, L), np.int64)     # sink tokens written
-        self._qlen = np.zeros((n, L), np.int64)     # tokens in the key/value buffers
-        self._npages = np.zeros((n, L), np.int64)   # pages of (slot, layer)
+        self._qlen = np.zeros((n, L), np.int64)     # keys in the key buffer
+        self._npages = np.zeros((n, L), np.int64)   # key pages of (slot, layer)
+        self._npv = np.zeros((n, L), np.int64)      # pages whose value half is written
+        self._vlen = np.zeros((n, L), np.int64)     # values in the value buffer
         # device counters (kind, layer, slot): a (layer, slot range) is a contiguous (B,) int32 view
-        self.lens = torch.zeros(3, L, n, dtype=torch.int32, device=dev)
+        self.lens = torch.zeros(5, L, n, dtype=torch.int32, device=dev)
         self._overflow = torch.zeros(n, dtype=torch.int32, device=dev)
         self.max_pages_per_seq = (config.max_seq_len - S) // G + 2
         self._block_table = torch.zeros(L, n, self.max_pages_per_seq, dtype=torch.int32, device=dev)
+        self._pages = np.zeros((n, L, self.max_pages_per_seq), np.int64)   # host mirror of the block table
         self._slot_of: Dict[int, int] = {}
         self._seq_of: Dict[int, int] = {}
         self._slots_dev: Dict[Tuple[int, ...], torch.Tensor] = {}
@@ -116,11 +131,14 @@ class KittyInferencePipeline:
 
     @property
     def val_local_len(self) -> int:
-        return int(self._qlen[self._slot0(), 0])
+        """Values in the R-token window (pipeline.py:103)."""
+        return int(min(self._vlen[self._slot0(), 0], self.config.local_value_window))
 
     @property
     def val_qbuf_len(self) -> int:
-        return 0
+        """FP16 values older than the window, waiting to be quantised (pipeline.py:108)."""
+        v = int(self._vlen[self._slot0(), 0])
+        return v - min(v, self.config.local_value_window)
 
     @property
     def sink_k(self) -> torch.Tensor:
@@ -136,22 +154,34 @@ class KittyInferencePipeline:
 
     @property
     def val_local(self) -> torch.Tensor:
-        return self._qbuf_v[self._slot0()]
+        """Sequence 0's FP16 value buffer, (L, H, R + G, D): the window and the
+        values waiting to be quantised, oldest first."""
+        return self._vbuf[self._slot0()]
 
-    # -------------------------------------------------------------- push
-    def push_token(self, layer_id: int, key: torch.Tensor, value: torch.Tensor, seq_id: int = 0) -> None:
-        """One (num_kv_heads, head_dim) token for one sequence (pipeline.py:115-181)."""
-        self.push_tokens(layer_id, key.unsqueeze(0), value.unsqueeze(0), [seq_id])
+    # ---------------------------------------------------- host -> device
+    def _h2d(self, a) -> torch.Tensor:
+        """Small int32 host data on the device without a blocking copy: a
+        pinned staging tensor (torch's host cache recycles it once the copy
+        has run) and a non-blocking copy on the current stream."""
+        t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32))
+        if self.device.type != "cuda":
+            return t
+        return t.pin_memory().to(self.device, non_blocking=True)
 
     def _slots_tensor(self, slots: np.ndarray) -> torch.Tensor:
         key = tuple(int(s) for s in slots)
         t = self._slots_dev.get(key)
         if t is None:
-            t = torch.tensor(list(key), dtype=torch.int32).to(self.device)
+            t = self._h2d(np.array(key, np.int32))
             if len(self._slots_dev) > 64:
                 self._slots_dev.clear()
             self._slots_dev[key] = t
         return t
+
+    # -------------------------------------------------------------- push
+    def push_token(self, layer_id: int, key: torch.Tensor, value: torch.Tensor, seq_id: int = 0) -> None:
+        """One (num_kv_heads, head_dim) token for one sequence (pipeline.py:115-181)."""
+        self.push_tokens(layer_id, key.unsqueeze(0), value.unsqueeze(0), [seq_id])
 
     def push_tokens(self, layer_id: int, keys: torch.Tensor, values: torch.Tensor, seq_ids: Sequence[int]) -> None:
         """One token for each of B sequences: keys / values (B, num_kv_heads, head_dim)."""
@@ -172,15 +202,17 @@ class KittyInferencePipeline:
         self._fill[slots[in_sink], l] += 1
         rows = np.nonzero(~in_sink)[0]
         self._qlen[slots[rows], l] += 1
-        full = rows[self._qlen[slots[rows], l] == G]
-        if len(full):
-            self._spill(l, slots[full], [seq_ids[i] for i in full])
+        self._vlen[slots[rows], l] += 1
+        kfull = rows[self._qlen[slots[rows], l] == G]
+        vfull = rows[self._vlen[slots[rows], l] == self.value_capacity]
+        if len(kfull) or len(vfull):
+            self._spill(l, slots[kfull], [seq_ids[i] for i in kfull], slots[vfull])
 
     def _append_device(self, l: int, keys: torch.Tensor, values: torch.Tensor, slots: np.ndarray) -> None:
         """kitty_append_tokens: every sequence's token into its buffers, one launch."""
         keys = keys if keys.stride(-1) == 1 else keys.contiguous()
         values = values if values.stride(-1) == 1 else values.contiguous()
-        sk, sv, qk, qv = (t[:, l] for t in (self._sink_k, self._sink_v, self._qbuf_k, self._qbuf_v))
+        sk, sv, qk, vb = (t[:, l] for t in (self._sink_k, self._sink_v, self._qbuf_k, self._vbuf))
         a = _hip.AppendArgs()
         a.key, a.value = keys.data_ptr(), values.data_ptr()
         a.key_s_seq, a.key_s_head = keys.stride(0), keys.stride(1)
@@ -189,10 +221,14 @@ class KittyInferencePipeline:
         a.slots = slots_dev.data_ptr()
         a.sink_k, a.sink_v = sk.data_ptr(), sv.data_ptr()
         a.sink_layout = _hip.SlotLayout(sk.stride(0), sk.stride(1), sk.stride(2))
-        a.buf_k, a.buf_v = qk.data_ptr(), qv.data_ptr()
+        a.buf_k = qk.data_ptr()
         a.buf_layout = _hip.SlotLayout(qk.stride(0), qk.stride(1), qk.stride(2))
         a.sink_fill = self.lens[_FILL, l].data_ptr()
         a.buf_len = self.lens[_QLEN, l].data_ptr()
+        a.val_len = self.lens[_VLEN, l].data_ptr()
+        a.val_buf = vb.data_ptr()
+        a.val_layout = _hip.SlotLayout(vb.stride(0), vb.stride(1), vb.stride(2))
+        a.val_tokens = self.value_capacity
         a.overflow = self._overflow.data_ptr()
         a.batch, a.num_kv_heads, a.head_dim = len(slots), keys.shape[1], keys.shape[2]
         a.sink_size, a.buf_tokens, a.num_slots = self.config.sink_size, self.config.q_buffer_size, self.num_slots
@@ -209,10 +245,10 @@ class KittyInferencePipeline:
                 self._sink_v[s, l, :, fill[i]] = values[i]
                 self.lens[_FILL, l, s] += 1
             else:
-                q = int(self._qlen[s, l])
-                self._qbuf_k[s, l, :, q] = keys[i]
-                self._qbuf_v[s, l, :, q] = values[i]
+                self._qbuf_k[s, l, :, int(self._qlen[s, l])] = keys[i]
+                self._vbuf[s, l, :, int(self._vlen[s, l])] = values[i]
                 self.lens[_QLEN, l, s] += 1
+                self.lens[_VLEN, l, s] += 1
 
     def overflowed(self) -> bool:
         """True if an append ever found a full, unspilled buffer (reads the device)."""
@@ -224,22 +260,47 @@ class KittyInferencePipeline:
             raise RuntimeError(f"sequence {seq_id} exceeds max_seq_len={self.config.max_seq_len}")
         return [self.layout.allocate_page(seq_id, layer, first + i).physical_idx for i in range(count)]
 
-    def _spill(self, layer: int, slots: np.ndarray, seq_ids: List[int]) -> None:
-        """Quantise the full key/value buffers of these slots into one new page
-        each (pipeline.py:183-256, one launch)."""
-        phys = [self._alloc(layer, s, seq, 1)[0] for s, seq in zip(slots.tolist(), seq_ids)]
+    def _spill(self, layer: int, kslots: np.ndarray, seq_ids: List[int], vslots: np.ndarray) -> None:
+        """Key spill of kslots (their full key buffers into one new page each)
+        and value spill of vslots (the oldest G values into the value half of
+        their first value-less page) (pipeline.py:183-256).  One launch each;
+        one launch for both when R = 0 (the same slots and pages)."""
         if self._store is None:
             raise RuntimeError("kitty (MI355X build) quantises only on ROCm devices")
-        sl = torch.as_tensor(slots, device=self.device)
-        pages = torch.tensor(phys, dtype=torch.int32).to(self.device)
-        kblk = self._qbuf_k[:, layer].index_select(0, sl)   # (n, H, G, D)
-        vblk = self._qbuf_v[:, layer].index_select(0, sl)
-        quantize_into_pools(self._store, kblk, vblk, self.boost_idx_uint8[layer], pages, self.config.sentinel)
-        self._block_table[layer, sl, torch.as_tensor(self._npages[slots, layer], device=self.device)] = pages
-        self._npages[slots, layer] += 1
-        self._qlen[slots, layer] = 0
-        self.lens[_QLEN, layer, sl] = 0
-        self.lens[_NPAGES, layer, sl] += 1
+        G, R = self.config.q_buffer_size, self.config.local_value_window
+        both = R == 0
+        if len(kslots):
+            phys = [self._alloc(layer, s, seq, 1)[0] for s, seq in zip(kslots.tolist(), seq_ids)]
+            pno = self._npages[kslots, layer]
+            self._pages[kslots, layer, pno] = phys
+            meta = self._h2d(np.stack([kslots, pno, np.asarray(phys)]))   # one copy: slots, page numbers, ids
+            sl, pn, pages = meta[0].long(), meta[1].long(), meta[2]
+            kblk = self._qbuf_k[:, layer].index_select(0, sl)             # (n, H, G, D)
+            vblk = self._vbuf[:, layer].index_select(0, sl)[:, :, :G] if both else None
+            quantize_into_pools(self._store, kblk, vblk, self.boost_idx_uint8[layer], pages, self.config.sentinel)
+            self._block_table[layer, sl, pn] = pages
+            self._npages[kslots, layer] += 1
+            self._qlen[kslots, layer] = 0
+            self.lens[_QLEN, layer, sl] = 0
+            self.lens[_NPAGES, layer, sl] += 1
+            if both:
+                self._npv[kslots, layer] += 1
+                self._vlen[kslots, layer] = 0
+                self.lens[_NPAGES_V, layer, sl] += 1
+                self.lens[_VLEN, layer, sl] = 0
+        if len(vslots) and not both:
+            phys = self._pages[vslots, layer, self._npv[vslots, layer]]
+            meta = self._h2d(np.stack([vslots, phys]))
+            sl, pages = meta[0].long(), meta[1]
+            vb = self._vbuf[:, layer]                                     # (slots, H, R + G, D)
+            vblk = vb.index_select(0, sl)                                 # a copy: the shift below may reuse rows
+            quantize_into_pools(self._store, None, vblk[:, :, :G], None, pages, self.config.sentinel)
+            if R:
+                vb[sl, :, :R] = vblk[:, :, G:G + R]                       # the R newest values move to the front
+            self._npv[vslots, layer] += 1
+            self._vlen[vslots, layer] -= G
+            self.lens[_NPAGES_V, layer, sl] += 1
+            self.lens[_VLEN, layer, sl] -= G
 
     # ------------------------------------------------------------ prefill
     def push_chunk(self, layer_id: int, keys: torch.Tensor, values: torch.Tensor, seq_ids: Sequence[int]) -> None:
@@ -248,7 +309,7 @@ class KittyInferencePipeline:
         push_tokens calls would leave (same sinks, buffers and page contents),
         with every complete page of the chunk quantised straight from it."""
         cfg = self.config
-        S, G = cfg.sink_size, cfg.q_buffer_size
+        S, G, R = cfg.sink_size, cfg.q_buffer_size, cfg.local_value_window
         keys = keys.to(self.device, torch.float16)
         values = values.to(self.device, torch.float16)
         T = keys.shape[2]
@@ -263,54 +324,79 @@ class KittyInferencePipeline:
                 self._sink_v[s, l, :, f:f + n_s] = values[i, :, :n_s]
                 self._fill[s, l] += n_s
                 t = n_s
-            q = int(self._qlen[s, l])
-            if t < T and q > 0:   # top up a partly filled buffer
-                n_q = min(T - t, G - q)
-                self._qbuf_k[s, l, :, q:q + n_q] = keys[i, :, t:t + n_q]
-                self._qbuf_v[s, l, :, q:q + n_q] = values[i, :, t:t + n_q]
-                t += n_q
-                self._qlen[s, l] += n_q
-                self.lens[_QLEN, l, s] = int(self._qlen[s, l])
-                if self._qlen[s, l] == G:
-                    self._spill(l, np.array([s]), [seq])
-            n_full = (T - t) // G
-            if n_full:
-                phys = self._alloc(l, s, seq, n_full)
-                if self._store is None:
-                    raise RuntimeError("kitty (MI355X build) quantises only on ROCm devices")
-                blk_k = keys[i, :, t:t + n_full * G].unflatten(1, (n_full, G)).transpose(0, 1)  # (n, H, G, D)
-                blk_v = values[i, :, t:t + n_full * G].unflatten(1, (n_full, G)).transpose(0, 1)
-                pages = torch.tensor(phys, dtype=torch.int32).to(self.device)
-                quantize_into_pools(self._store, blk_k, blk_v, self.boost_idx_uint8[l], pages, cfg.sentinel)
-                p0 = int(self._npages[s, l])
-                self._block_table[l, s, p0:p0 + n_full] = pages
-                self._npages[s, l] += n_full
-                t += n_full * G
-            rem = T - t
-            if rem:
-                self._qbuf_k[s, l, :, :rem] = keys[i, :, t:]
-                self._qbuf_v[s, l, :, :rem] = values[i, :, t:]
+            m = T - t
+            if m:
+                # keys: buffered keys + the chunk, cut into full pages and a new buffer
+                nk = int(self._qlen[s, l])
+                kall = torch.cat([self._qbuf_k[s, l, :, :nk], keys[i, :, t:]], dim=1)   # (H, nk + m, D)
+                n_full = (nk + m) // G
+                if n_full:
+                    if self._store is None:
+                        raise RuntimeError("kitty (MI355X build) quantises only on ROCm devices")
+                    phys = self._alloc(l, s, seq, n_full)
+                    p0 = int(self._npages[s, l])
+                    self._pages[s, l, p0:p0 + n_full] = phys
+                    pages = self._h2d(np.asarray(phys))
+                    blk_k = kall[:, :n_full * G].unflatten(1, (n_full, G)).transpose(0, 1)   # (n, H, G, D)
+                    vblk = None
+                    if R == 0:   # values leave FP16 with their keys
+                        nv = int(self._vlen[s, l])
+                        vall = torch.cat([self._vbuf[s, l, :, :nv], values[i, :, t:]], dim=1)
+                        vblk = vall[:, :n_full * G].unflatten(1, (n_full, G)).transpose(0, 1)
+                    quantize_into_pools(self._store, blk_k, vblk, self.boost_idx_uint8[l], pages, cfg.sentinel)
+                    self._block_table[l, s, p0:p0 + n_full] = pages
+                    self._npages[s, l] += n_full
+                    if R == 0:
+                        self._npv[s, l] += n_full
+                rem = nk + m - n_full * G
+                self._qbuf_k[s, l, :, :rem] = kall[:, n_full * G:]
                 self._qlen[s, l] = rem
-            self.lens[:, l, s] = torch.tensor([int(self._fill[s, l]), int(self._qlen[s, l]),
-                                               int(self._npages[s, l])], dtype=torch.int32).to(self.device)
+                # values: buffered values + the chunk; full pages spill while
+                # more than R values would stay behind
+                nv = int(self._vlen[s, l])
+                vall = torch.cat([self._vbuf[s, l, :, :nv], values[i, :, t:]], dim=1)        # (H, nv + m, D)
+                if R == 0:
+                    v_full = n_full
+                else:
+                    v_full = max(0, (nv + m - R) // G)
+                    if v_full:
+                        pv0 = int(self._npv[s, l])
+                        pages_v = self._h2d(self._pages[s, l, pv0:pv0 + v_full])
+                        blk_v = vall[:, :v_full * G].unflatten(1, (v_full, G)).transpose(0, 1)
+                        quantize_into_pools(self._store, None, blk_v, None, pages_v, cfg.sentinel)
+                        self._npv[s, l] += v_full
+                vrem = nv + m - v_full * G
+                self._vbuf[s, l, :, :vrem] = vall[:, v_full * G:]
+                self._vlen[s, l] = vrem
+            self.lens[:, l, s] = self._h2d(np.array([self._fill[s, l], self._qlen[s, l], self._npages[s, l],
+                                                     self._npv[s, l], self._vlen[s, l]]))
 
     # ------------------------------------------------------------- query
     def get_attention_context(self, layer_id: int, seq_id: int = 0) -> dict:
-        """FP16 segments and ordered page list of one sequence (pipeline.py:260-282)."""
+        """FP16 segments and ordered page list of one sequence
+        (pipeline.py:260-282): the key pages, the FP16 key buffer, and the
+        FP16 values not yet in pages (val_local: the values of the last
+        value_pages * G ... n tokens, oldest first) with the number of pages
+        whose value half holds values (value_pages)."""
         s = self.slot(seq_id)
-        f, q = int(self._fill[s, layer_id]), int(self._qlen[s, layer_id])
+        f, q, v = int(self._fill[s, layer_id]), int(self._qlen[s, layer_id]), int(self._vlen[s, layer_id])
         return {
             "sink_k": self._sink_k[s, layer_id, :, :f],
             "sink_v": self._sink_v[s, layer_id, :, :f],
             "key_qbuf": self._qbuf_k[s, layer_id, :, :q],
-            "val_local": self._qbuf_v[s, layer_id, :, :q],
+            "val_local": self._vbuf[s, layer_id, :, :v],
             "page_list": self.layout.get_page_list(seq_id=seq_id, layer_id=layer_id),
+            "value_pages": int(self._npv[s, layer_id]),
         }
 
-    def decode_inputs(self, layer_id: int, seq_ids: Sequence[int]) -> dict:
+    def decode_inputs(self, layer_id: int, seq_ids: Sequence[int], full_width: bool = False) -> dict:
         """Batched decode operands for the sequences' slots: block table rows,
-        page counts and FP16 sink / tail views with their lengths, read from
-        the device-side state (views, no copies, for a contiguous slot range)."""
+        key / value page counts and FP16 sink / key-tail / value-tail views
+        with their lengths, read from the device-side state (views, no
+        copies, for a contiguous slot range: then `contiguous` is True and
+        the views stay valid for later steps).  With R = 0 the value stream is
+        the key stream's (num_pages_v / tail_len_v None).  max_pages is the
+        batch's largest page count, or the table width with full_width."""
         slots = np.array([self.slot(s) for s in seq_ids], np.int64)
         contiguous = bool(len(slots) and (np.diff(slots) == 1).all())
         lens = self.lens[:, layer_id]
@@ -322,10 +408,16 @@ class KittyInferencePipeline:
             idx = self._slots_tensor(slots).long()
             pick = lambda t: t[:, layer_id].index_select(0, idx)
             lens = lens.index_select(1, idx)
+        split = self.config.local_value_window > 0
+        if full_width:
+            max_pages = self.max_pages_per_seq
+        else:
+            max_pages = int(self._npages[slots, layer_id].max()) if len(slots) else 0
         return dict(block_table=pick(self._block_table.transpose(0, 1)), num_pages=lens[_NPAGES],
                     sink_k=pick(self._sink_k), sink_v=pick(self._sink_v), sink_len=lens[_FILL],
-                    tail_k=pick(self._qbuf_k), tail_v=pick(self._qbuf_v), tail_len=lens[_QLEN],
-                    max_pages=int(self._npages[slots, layer_id].max()) if len(slots) else 0)
+                    tail_k=pick(self._qbuf_k), tail_v=pick(self._vbuf), tail_len=lens[_QLEN],
+                    num_pages_v=lens[_NPAGES_V] if split else None, tail_len_v=lens[_VLEN] if split else None,
+                    max_pages=max_pages, contiguous=contiguous)
 
     # ------------------------------------------------------------- reset
     def reset_sequence(self, seq_id: int = 0) -> None:
@@ -335,11 +427,11 @@ class KittyInferencePipeline:
         if s is None:
             return
         self._seq_of.pop(s, None)
-        self._fill[s] = 0
-        self._qlen[s] = 0
-        self._npages[s] = 0
+        for c in (self._fill, self._qlen, self._npages, self._npv, self._vlen):
+            c[s] = 0
+        self._pages[s] = 0
         self.lens[:, :, s] = 0
-        for t in (self._sink_k, self._sink_v, self._qbuf_k, self._qbuf_v, self._block_table.transpose(0, 1)):
+        for t in (self._sink_k, self._sink_v, self._qbuf_k, self._vbuf, self._block_table.transpose(0, 1)):
             t[s].zero_()
 
     def stats(self) -> dict:

@@ -1,10 +1,13 @@
 """Pipeline and drop-in module on the GPU.
 
 * the reference's pipeline-state tests (tests/test_attention.py:57-126);
-* page bytes after spills are the oracle quantisation of the same tokens;
+* page bytes after spills are the oracle quantisation of the same tokens
+  (keys of every page, values of the pages older than the value window) and
+  the FP16 value buffer holds the newest values;
 * KittyPagedAttention decode end to end against the oracle computed from the
-  raw token history (sinks, pages and tail derived independently), including
-  BASELINE config 1 (B1, 8Q/8KV, d128, context 1024, outlier key channels).
+  raw token history (sinks, key pages, value pages, key and value tails
+  derived independently from n, G and the window R), including BASELINE
+  config 1 (B1, 8Q/8KV, d128, context 1024, outlier key channels).
 """
 import numpy as np
 import pytest
@@ -56,9 +59,15 @@ def test_reference_pipeline_state(dev):
     for _ in range(G - 3):
         p.push_token(0, *_tok(H, D, gen))
     assert p.key_qbuf_len == 0 and len(lay.get_page_list(0, 0)) == 1   # :86-99
-    for _ in range(2 * G):
+    # the window (R = G = 8): values stay FP16 until they are R tokens old
+    assert p.val_local_len == 8 and p.val_qbuf_len == 0
+    for _ in range(4):
+        p.push_token(0, *_tok(H, D, gen))
+    assert p.val_local_len == 8 and p.val_qbuf_len == 4 and p.get_attention_context(0)["value_pages"] == 0
+    for _ in range(2 * G - 4):
         p.push_token(0, *_tok(H, D, gen))
     assert len(lay.get_page_list(0, 0)) == 3                  # :115-126
+    assert p.get_attention_context(0)["value_pages"] == 2 and p.val_local_len == 8 and p.val_qbuf_len == 0
     p.reset_sequence(0)
     assert p.sink_fill == 0 and p.key_qbuf_len == 0 and lay.memory_stats()["pages_used"] == 0  # :101-113
 
@@ -86,11 +95,21 @@ def test_spilled_pages_are_bit_exact(dev):
     torch.cuda.synchronize()
     kb, kh, km, vp, vm = [t.cpu().numpy() for t in (lay.key_baseline, lay.key_boost, lay.key_metadata,
                                                      lay.value_pool, lay.value_metadata)]
+    R = cfg.local_value_window
     for s in n_tok:
         for l in range(L):
             toks = [(k, v) for (ll, k, v) in hist[s] if ll == l]
             pages = lay.get_page_list(s, l)
-            assert len(pages) == (n_tok[s] - S) // G
+            n = n_tok[s] - S
+            assert len(pages) == n // G
+            npv = max(0, n - R) // G
+            slot = p.slot(s)
+            assert int(p._npv[slot, l]) == npv and int(p._vlen[slot, l]) == max(0, n) - npv * G
+            # the FP16 value buffer: the values of tokens npv G .. n, oldest first
+            vb = p._vbuf[slot, l, :, :max(0, n) - npv * G].cpu()
+            want = [v for _, v in toks[S + npv * G:]]
+            if want:
+                assert torch.equal(vb, torch.stack(want).transpose(0, 1))
             for pi, ph in enumerate(pages):
                 blk = toks[S + pi * G: S + (pi + 1) * G]
                 K = torch.stack([k for k, _ in blk]).numpy()   # (G, H, D)
@@ -100,16 +119,21 @@ def test_spilled_pages_are_bit_exact(dev):
                     assert np.array_equal(kb[ph, h], e[0]) and np.array_equal(kh[ph, h], e[1])
                     assert np.array_equal(km[ph, h, 0].astype(np.float32), e[2].astype(np.float32))
                     assert np.array_equal(km[ph, h, 1].astype(np.float32), e[3].astype(np.float32))
+                    if pi >= npv:
+                        continue      # values still FP16 (in the window)
                     ev = O.quantize_value(V[:, h].copy())
                     assert np.array_equal(vp[ph, h], ev[0])
                     assert np.array_equal(vm[ph, h, :, 0].astype(np.float32), ev[1].astype(np.float32))
 
 
-def _oracle_from_history(K, V, q, S, G, bi, d_boost, sentinel, Hq, H, D):
-    """Independent oracle: sinks / pages / tail cut from the raw token history."""
+def _oracle_from_history(K, V, q, S, G, bi, d_boost, sentinel, Hq, H, D, R=0):
+    """Independent oracle: sinks / key pages / value pages / key and value
+    tails cut from the raw token history (values of the last R tokens, and
+    of the rest of their G-token block, stay FP16)."""
     T = K.shape[0]
     ns = min(S, T)
     npg = max(0, (T - S) // G)
+    npv = max(0, T - S - R) // G
     P = max(npg, 1)
     kb = np.zeros((P, H, D, G // 4), np.uint8)
     kh = np.zeros((P, H, d_boost, G // 4), np.uint8)
@@ -123,9 +147,14 @@ def _oracle_from_history(K, V, q, S, G, bi, d_boost, sentinel, Hq, H, D):
                                                                                sentinel)
             vp[pi, h], vm[pi, h, :, 0], vm[pi, h, :, 1] = O.quantize_value(V[blk, h].copy())
     tail = slice(S + npg * G, T)
-    return O.paged_attention(q, np.arange(npg), kb, kh, km, vp, vm, bi, d_boost,
-                             K[:ns].transpose(1, 0, 2).copy(), V[:ns].transpose(1, 0, 2).copy(),
-                             K[tail].transpose(1, 0, 2).copy(), V[tail].transpose(1, 0, 2).copy(), Hq, H, D)
+    if npv == npg:
+        return O.paged_attention(q, np.arange(npg), kb, kh, km, vp, vm, bi, d_boost,
+                                 K[:ns].transpose(1, 0, 2).copy(), V[:ns].transpose(1, 0, 2).copy(),
+                                 K[tail].transpose(1, 0, 2).copy(), V[tail].transpose(1, 0, 2).copy(), Hq, H, D)
+    vtail = slice(S + npv * G, T)
+    return O.paged_attention_kv(q, np.arange(npg), np.arange(npv), kb, kh, km, vp, vm, bi, d_boost,
+                                K[:ns].transpose(1, 0, 2).copy(), V[:ns].transpose(1, 0, 2).copy(),
+                                K[tail].transpose(1, 0, 2).copy(), V[vtail].transpose(1, 0, 2).copy(), Hq, H, D)
 
 
 def _close(got, ref):
@@ -157,16 +186,19 @@ def test_config1_module_decode_step(dev):
     out = attn(q.to(dev), K[1023:].permute(1, 0, 2)[None].to(dev), V[1023:].permute(1, 0, 2)[None].to(dev))
     assert out.shape == (1, Hq, 1, D) and out.dtype == torch.float16
     ref = _oracle_from_history(K.numpy(), V.numpy(), q[0, :, 0].numpy(), 32, 128, bi.numpy(), cfg.d_boost,
-                               cfg.sentinel, Hq, H, D)
+                               cfg.sentinel, Hq, H, D, R=128)
     _close(out[0, :, 0].cpu().numpy(), ref)
 
 
 def test_batched_module_decode_gqa(dev):
     """Three sequences of different lengths decoded together through the
-    module (GQA 4, MFMA path), checked per sequence against the oracle."""
+    module (GQA 4, MFMA path, 128-token value window: key pages run one
+    ahead of value pages once a sequence passes 256 tokens), checked per
+    sequence against the oracle.  The cached decode plan is reused across
+    the steps and rebuilt when the batch changes."""
     from kitty import KittyAttentionFactory
     cfg = _cfg(num_kv_heads=2, head_dim=128, q_buffer_size=128, sink_size=32, boost_rate=0.125,
-               max_seq_len=1024, max_batch_size=3)
+               local_value_window=128, max_seq_len=1024, max_batch_size=3)
     H, D, Hq = 2, 128, 8
     gen = torch.Generator().manual_seed(12)
     bi = torch.full((1, H, D), cfg.sentinel, dtype=torch.uint8)
@@ -190,7 +222,7 @@ def test_batched_module_decode_gqa(dev):
                 Kh = torch.stack([a for a, _ in hist[s]]).numpy()
                 Vh = torch.stack([b for _, b in hist[s]]).numpy()
                 ref = _oracle_from_history(Kh, Vh, q[i, :, 0].numpy(), 32, 128, bi[0].numpy(), cfg.d_boost,
-                                           cfg.sentinel, Hq, H, D)
+                                           cfg.sentinel, Hq, H, D, R=128)
                 _close(out[i, :, 0].cpu().numpy(), ref)
 
 
@@ -220,13 +252,16 @@ def _logical_pages(p, lay, seq, layer):
     return out
 
 
-@pytest.mark.parametrize("D,G,S,pre,T", [(16, 8, 4, 0, 61), (16, 8, 4, 6, 50), (128, 128, 32, 0, 700),
-                                         (128, 128, 32, 45, 400)])
-def test_bulk_prefill_matches_token_pushes(dev, D, G, S, pre, T):
+@pytest.mark.parametrize("D,G,S,pre,T,R", [(16, 8, 4, 0, 61, 8), (16, 8, 4, 6, 50, 8), (16, 8, 4, 3, 70, 5),
+                                           (16, 8, 4, 6, 50, 0), (128, 128, 32, 0, 700, 128),
+                                           (128, 128, 32, 45, 400, 128), (128, 128, 32, 45, 400, 0)])
+def test_bulk_prefill_matches_token_pushes(dev, D, G, S, pre, T, R):
     """push_chunk (bulk prefill: sinks and buffer rows copied, complete pages
     quantised straight from the chunk) leaves exactly the state of T single
-    pushes: same sinks, buffers, counters (host and device), page bytes."""
-    cfg = _cfg(num_layers=2, num_kv_heads=2, head_dim=D, q_buffer_size=G, sink_size=S, local_value_window=G,
+    pushes: same sinks, key and value buffers, counters (host and device),
+    page bytes; for value windows R = G, R = 0 (the single stream) and an R
+    that is not a multiple of G."""
+    cfg = _cfg(num_layers=2, num_kv_heads=2, head_dim=D, q_buffer_size=G, sink_size=S, local_value_window=R,
                boost_rate=0.125, max_batch_size=2)
     gen = torch.Generator().manual_seed(D + T)
     B, H = 2, cfg.num_kv_heads
@@ -242,20 +277,21 @@ def test_bulk_prefill_matches_token_pushes(dev, D, G, S, pre, T):
             a.push_tokens(layer, K[:, :, t], V[:, :, t], [0, 1])
         b.push_chunk(layer, K[:, :, pre:], V[:, :, pre:], [0, 1])
     torch.cuda.synchronize()
-    assert np.array_equal(a._fill, b._fill) and np.array_equal(a._qlen, b._qlen)
-    assert np.array_equal(a._npages, b._npages)
+    for c in ("_fill", "_qlen", "_npages", "_npv", "_vlen"):
+        assert np.array_equal(getattr(a, c), getattr(b, c)), c
     assert torch.equal(a.lens, b.lens)
-    assert np.array_equal(a.lens[0].cpu().numpy().T, a._fill)
-    assert np.array_equal(a.lens[1].cpu().numpy().T, a._qlen)
-    assert np.array_equal(a.lens[2].cpu().numpy().T, a._npages)
+    for i, c in enumerate(("_fill", "_qlen", "_npages", "_npv", "_vlen")):
+        assert np.array_equal(a.lens[i].cpu().numpy().T, getattr(a, c)), c
+    # the two streams cover the same tokens: (P_k - P_v) G + n_k = n_v
+    assert np.array_equal((a._npages - a._npv) * G + a._qlen, a._vlen)
     for layer in range(2):
         for seq in range(B):
             s = a.slot(seq)
-            f, q = int(a._fill[s, layer]), int(a._qlen[s, layer])
+            f, q, v = int(a._fill[s, layer]), int(a._qlen[s, layer]), int(a._vlen[s, layer])
             assert torch.equal(a._sink_k[s, layer, :, :f], b._sink_k[s, layer, :, :f])
             assert torch.equal(a._sink_v[s, layer, :, :f], b._sink_v[s, layer, :, :f])
             assert torch.equal(a._qbuf_k[s, layer, :, :q], b._qbuf_k[s, layer, :, :q])
-            assert torch.equal(a._qbuf_v[s, layer, :, :q], b._qbuf_v[s, layer, :, :q])
+            assert torch.equal(a._vbuf[s, layer, :, :v], b._vbuf[s, layer, :, :v])
             pa, pb = _logical_pages(a, lay_a, seq, layer), _logical_pages(b, lay_b, seq, layer)
             assert len(pa) == len(pb) == int(a._npages[s, layer])
             for x, y in zip(pa, pb):
