@@ -335,6 +335,137 @@ def bench_quantize(torch, dev, reps: int = 64, cpu: bool = False) -> dict:
     return out
 
 
+def module_leg(torch, dev, cfg_name: str = "cfg3", cycles: int = 2) -> dict:
+    """KittyPagedAttention.forward decode steps at a config's shape, the
+    drop-in module path: per step one token of every sequence through the
+    pipeline (append; key and value spills every G steps) and the fused
+    decode over key pages, value pages (128-token value window) and FP16
+    tails.  Sequences are prefilled to ctx - 2G tokens with push_chunk and
+    run G untimed steps (one spill cycle: the first launch of every kernel
+    and the first pinned staging buffer are set-up costs), then `cycles` x G
+    steps are timed back to back (host clock, events on the stream), so each
+    sequence spills its keys and values `cycles` times.  A last pass with an
+    event per step separates the spill steps."""
+    from kitty import KittyConfig, KittyAttentionFactory
+    c = CONFIGS[cfg_name]
+    B, Hq, Hkv, ctx = c["B"], c["Hq"], c["Hkv"], c["ctx"]
+    kcfg = KittyConfig(num_layers=1, num_kv_heads=Hkv, head_dim=D, q_buffer_size=G, sink_size=S,
+                       local_value_window=128, boost_rate=c["boost"], max_seq_len=ctx + (cycles + 2) * G,
+                       max_batch_size=B, device=str(dev))
+    gen = torch.Generator(device="cpu").manual_seed(c["seed"])
+    dk = kcfg.d_boost
+    bi = torch.full((1, Hkv, D), kcfg.sentinel, dtype=torch.uint8)
+    scale = torch.ones(Hkv, D)
+    for h in range(Hkv):
+        ch = torch.randperm(D, generator=gen)[:dk]
+        bi[0, h, ch] = torch.arange(dk, dtype=torch.uint8)
+        scale[h, ch] = c["outlier"]
+    layout, pipe, layers = KittyAttentionFactory.from_config(kcfg, bi, Hq)
+    attn = layers[0]
+    g = torch.Generator(device=dev).manual_seed(c["seed"] + 200)
+    scale = scale.to(dev)
+    pre = ctx - 2 * G                   # warm-up and timed steps take every sequence across ctx
+    chunk = 4096
+    for t0 in range(0, pre, chunk):
+        n = min(chunk, pre - t0)
+        k = (torch.randn(B, Hkv, n, D, device=dev, generator=g) * scale[None, :, None, :]).half()
+        v = torch.randn(B, Hkv, n, D, device=dev, generator=g).half()
+        pipe.push_chunk(0, k, v, list(range(B)))
+    steps = cycles * G
+    qs = torch.randn(steps, B, Hq, 1, D, device=dev, generator=g).half()
+    ks = (torch.randn(steps, B, Hkv, 1, D, device=dev, generator=g) * scale[None, None, :, None, :]).half()
+    vs = torch.randn(steps, B, Hkv, 1, D, device=dev, generator=g).half()
+    torch.cuda.synchronize()
+    seq_ids = list(range(B))
+    # one untimed spill cycle: builds and caches the decode plan, first launches
+    for i in range(G):
+        attn(qs[i % steps], ks[i % steps], vs[i % steps], seq_id=seq_ids)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        attn(qs[i], ks[i], vs[i], seq_id=seq_ids)
+    e1.record()
+    torch.cuda.synchronize()
+    n_t = steps
+    wall_us = (time.perf_counter() - t0) * 1e6 / n_t
+    event_us = e0.elapsed_time(e1) * 1e3 / n_t
+    # per-step events over one more cycle of G steps: spill steps vs the rest
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(G + 1)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for i in range(G):
+        attn(qs[i % steps], ks[i % steps], vs[i % steps], seq_id=seq_ids)
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(G)]
+    med = statistics.median(per)     # the sequences run in lockstep: one step of the G spills them all
+    worst = max(per)
+    plan = attn._plans.get(tuple(range(B)))
+    assert plan is not None, "the decode plan is cached across steps"
+    del layers, attn, pipe, layout, qs, ks, vs
+    torch.cuda.empty_cache()
+    return {"workload": f"KittyPagedAttention.forward decode, {cfg_name} shape: B{B} Hq{Hq} Hkv{Hkv} d{D}, "
+                        f"contexts {ctx - G + 1}..{ctx + (cycles - 1) * G}, S{S} G{G} R128 "
+                        f"{int(c['boost'] * 1000) / 10}% INT4 keys",
+            "us_per_step": round(wall_us, 2), "us_per_step_events": round(event_us, 2), "steps": n_t,
+            "step_us_median": round(med, 2), "spill_step_us": round(worst, 2),
+            "spill_step_extra_us": round(worst - med, 2),
+            "note": "each step: append of all B tokens, key/value spills every G steps (one key-only and one "
+                    "value-only batch-quantize launch over B*Hkv blocks plus the value-buffer shift), decode "
+                    "with independent key/value streams (streaming split kernel) and merge; host clock over "
+                    "the timed steps includes the Python module overhead"}
+
+
+def spill_latency(torch, dev, B: int = 16, Hkv: int = 8, dk: int = 16, reps: int = 64) -> dict:
+    """The pipeline's spill launches at their production shape: one
+    kitty_quantize_kv_blocks launch over the B * Hkv (G x D) blocks of one
+    layer (config-3 batch), key and value together (R = 0), key only and
+    value only (a 128-token value window), each timed as bursts of `reps`
+    back-to-back launches over 8 rotating input / page sets."""
+    from kitty.kernels.ops import QuantizePlan, pool_store
+    sets = 8
+    n = B * sets
+    pools = [torch.empty(n, Hkv, D, G // 4, dtype=torch.uint8, device=dev),
+             torch.empty(n, Hkv, dk, G // 4, dtype=torch.uint8, device=dev),
+             torch.empty(n, Hkv, 2, D, dtype=torch.float16, device=dev),
+             torch.empty(n, Hkv, G, D // 4, dtype=torch.uint8, device=dev),
+             torch.empty(n, Hkv, G, 2, dtype=torch.float16, device=dev)]
+    store = pool_store(*pools)
+    g = torch.Generator(device=dev).manual_seed(9)
+    bi = torch.full((Hkv, D), dk + 1, dtype=torch.uint8)
+    for h in range(Hkv):
+        bi[h, torch.randperm(D, generator=torch.Generator().manual_seed(h))[:dk]] = torch.arange(dk, dtype=torch.uint8)
+    bi = bi.to(dev)
+    res = {}
+    for kind in ("key+value", "key only", "value only"):
+        plans = []
+        for i in range(sets):
+            k = torch.randn(B, Hkv, G, D, device=dev, generator=g).half()
+            v = torch.randn(B, Hkv, G, D, device=dev, generator=g).half()
+            pids = torch.arange(i * B, (i + 1) * B, dtype=torch.int32, device=dev)
+            plans.append(QuantizePlan(store, k if kind != "value only" else None,
+                                      v if kind != "key only" else None,
+                                      bi if kind != "value only" else None, pids, dk + 1))
+        for p in plans:
+            p.run()
+        torch.cuda.synchronize()
+
+        def burst() -> float:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(reps):
+                plans[i % sets].run()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / reps * 1e3
+        res[kind] = round(statistics.median(burst() for _ in range(5)), 2)
+    return {"blocks": B * Hkv, "us_per_launch": res,
+            "workload": f"{B * Hkv} blocks of {G} tokens x {D} channels (B{B} x Hkv{Hkv}, one layer), {dk} INT4 "
+                        f"key channels"}
+
+
 def copy_probe(torch, dev) -> int:
     """A device-to-device copy of known size: its FETCH_SIZE / WRITE_SIZE
     counters per dispatch calibrate the decode kernel's counter readings."""
@@ -481,6 +612,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-quantize", action="store_true")
+    ap.add_argument("--no-module", action="store_true", help="skip the KittyPagedAttention.forward leg")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (HBM counter calibration)")
     args = ap.parse_args()
@@ -538,6 +670,10 @@ def main() -> int:
         result["legs"] = legs
     if not args.no_quantize:
         result["quantize_pack"] = bench_quantize(torch, dev, cpu=not args.no_cpu_baseline)
+        result["spill"] = spill_latency(torch, dev)
+    if not args.no_module:
+        log("timing KittyPagedAttention.forward decode steps")
+        result["module_forward"] = module_leg(torch, dev, "cfg3")
     print(json.dumps(result), flush=True)
     return 0
 
