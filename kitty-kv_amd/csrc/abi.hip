@@ -15,9 +15,9 @@ void set_error(const std::string &msg) { g_last_error = msg; }
 const char *get_error() { return g_last_error.c_str(); }
 
 // Waves of the decode kernels resident on the current device at once:
-// waves_per_cu per CU (streaming kernel: 16 for GQA groups of 4 and 8, with
-// 10 KB of LDS and 128 registers each, 8 for 16; page-pair MFMA kernel: 8
-// and 4), 4096 / 2048 on an MI355X.
+// waves_per_cu per CU (streaming kernel: 4 * KITTY_STREAM_WAVES_PER_EU for
+// GQA groups of 4 and 8, 8 for 16; page-pair MFMA kernel: 8 and 4), 3072 /
+// 2048 on an MI355X.
 static int64_t resident_waves(int waves_per_cu = 8)
 {
     int dev = 0, cus = 0;
@@ -79,7 +79,7 @@ static void set_plan(DecodeParams &p, const kitty_decode_args &a, bool balanced)
     p.fp16_weight = fp16_weight(p.GQ);
     p.fp16_units = seq_fp16_units(p.sink_cap + p.tail_v_cap, p.fp16_weight);
     const bool stream = uses_stream_kernel(p);
-    const int64_t res = resident_waves(stream ? (p.GQ <= 8 ? 16 : 8) : (p.GQ <= 8 ? 8 : 4));
+    const int64_t res = resident_waves(stream ? (p.GQ <= 8 ? 4 * KITTY_STREAM_WAVES_PER_EU : 8) : (p.GQ <= 8 ? 8 : 4));
     if (a.pages_per_split > 0) {
         p.min_chunk = a.pages_per_split;
         const int64_t pairs = (int64_t)a.batch * a.num_kv_heads;

@@ -10,6 +10,14 @@ constexpr int kChunkMax = 256; // tokens per softmax chunk in the generic path (
 // for a single K/V stream too.  It always runs when the value stream is
 // independent (num_pages_v given), which the page-pair kernel does not take.
 constexpr int KITTY_DECODE_STREAM_KERNEL = 1 << 30;
+
+// Waves per SIMD of the streaming kernel for GQA groups of 4 and 8 (its
+// occupancy and register budget; the work plan sizes its grid with it).
+// Three (168 registers, 12 waves and 120 KB of LDS per CU) measured faster
+// than four (128 registers, which spill): 67 vs 78 us at config 3.
+#ifndef KITTY_STREAM_WAVES_PER_EU
+#define KITTY_STREAM_WAVES_PER_EU 3
+#endif
 constexpr int kMaxPagesPerSplit = 64;
 
 struct DecodeParams {

@@ -1129,7 +1129,7 @@ struct SeqUnits {
 // per segment.  w is the workgroup's XCD-local order (xcd_local_index), so
 // the consecutive waves of a pair share an XCD and its L2.
 template <int GQ>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(GQ <= 8 ? 4 : 2)))
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(GQ <= 8 ? KITTY_STREAM_WAVES_PER_EU : 2)))
 void decode_stream_kernel(DecodeParams p)
 {
     __shared__ __attribute__((aligned(16))) unsigned char stage[kStage];
