@@ -278,6 +278,10 @@ extern "C" int kitty_quantize_kv_blocks(const kitty_page_store *store, const kit
     if (page128_supported(*store, qb))
         return launch_page128(L, (hipStream_t)stream);
     dim3 grid((unsigned)nblocks, 2);
+    // D * G = 32768 (e.g. D = 256, G = 128) needs ~76 KB of dynamic LDS
+    if (lds > 64 * 1024 && hipFuncSetAttribute((const void *)quantize_kv_kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return fail(KITTY_E_HIP, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
     hipLaunchKernelGGL(quantize_kv_kernel, grid, dim3(kQuantThreads), lds, (hipStream_t)stream, L);
     return check_launch("quantize_kv_kernel");
 }

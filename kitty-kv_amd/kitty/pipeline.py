@@ -193,20 +193,23 @@ class KittyInferencePipeline:
         keys = keys.to(self.device, torch.float16)
         values = values.to(self.device, torch.float16)
         l = layer_id
+        fill = self._fill[slots, l]
+        in_sink = fill < S
+        rows = np.nonzero(~in_sink)[0]
+        # sequences whose buffers this token fills: their new pages are taken
+        # first, all or nothing, so a full pool raises before any state changes
+        kfull = rows[self._qlen[slots[rows], l] + 1 == G]
+        vfull = rows[self._vlen[slots[rows], l] + 1 == self.value_capacity]
+        phys = self._alloc_spill(l, slots[kfull], [seq_ids[i] for i in kfull]) if len(kfull) else []
         if self._store is not None:
             self._append_device(l, keys, values, slots)
         else:
             self._append_host(l, keys, values, slots)
-        fill = self._fill[slots, l]
-        in_sink = fill < S
         self._fill[slots[in_sink], l] += 1
-        rows = np.nonzero(~in_sink)[0]
         self._qlen[slots[rows], l] += 1
         self._vlen[slots[rows], l] += 1
-        kfull = rows[self._qlen[slots[rows], l] == G]
-        vfull = rows[self._vlen[slots[rows], l] == self.value_capacity]
         if len(kfull) or len(vfull):
-            self._spill(l, slots[kfull], [seq_ids[i] for i in kfull], slots[vfull])
+            self._spill(l, slots[kfull], phys, slots[vfull])
 
     def _append_device(self, l: int, keys: torch.Tensor, values: torch.Tensor, slots: np.ndarray) -> None:
         """kitty_append_tokens: every sequence's token into its buffers, one launch."""
@@ -254,23 +257,38 @@ class KittyInferencePipeline:
         """True if an append ever found a full, unspilled buffer (reads the device)."""
         return bool(self._overflow.any().item())
 
-    def _alloc(self, layer: int, slot: int, seq_id: int, count: int) -> List[int]:
-        first = int(self._npages[slot, layer])
-        if first + count > self.max_pages_per_seq:
-            raise RuntimeError(f"sequence {seq_id} exceeds max_seq_len={self.config.max_seq_len}")
-        return [self.layout.allocate_page(seq_id, layer, first + i).physical_idx for i in range(count)]
-
-    def _spill(self, layer: int, kslots: np.ndarray, seq_ids: List[int], vslots: np.ndarray) -> None:
-        """Key spill of kslots (their full key buffers into one new page each)
-        and value spill of vslots (the oldest G values into the value half of
-        their first value-less page) (pipeline.py:183-256).  One launch each;
-        one launch for both when R = 0 (the same slots and pages)."""
+    def _alloc_spill(self, layer: int, slots: np.ndarray, seq_ids: Sequence[int],
+                     counts: Optional[Sequence[int]] = None) -> List[int]:
+        """Physical pages for the next key pages of these sequences (counts[i]
+        of them, default one each), all or nothing: on a full pool or a
+        sequence past max_seq_len the pages already taken are returned and
+        RuntimeError is raised."""
         if self._store is None:
             raise RuntimeError("kitty (MI355X build) quantises only on ROCm devices")
+        taken: List[Tuple[int, int, int]] = []
+        try:
+            for i, (s, seq) in enumerate(zip(np.asarray(slots).tolist(), seq_ids)):
+                first = int(self._npages[s, layer])
+                count = 1 if counts is None else int(counts[i])
+                if first + count > self.max_pages_per_seq:
+                    raise RuntimeError(f"sequence {seq} exceeds max_seq_len={self.config.max_seq_len}")
+                for j in range(count):
+                    taken.append((seq, first + j, self.layout.allocate_page(seq, layer, first + j).physical_idx))
+        except RuntimeError:
+            for seq, pno, _ in taken:
+                self.layout.free_page(seq, layer, pno)
+            raise
+        return [t[2] for t in taken]
+
+    def _spill(self, layer: int, kslots: np.ndarray, phys: List[int], vslots: np.ndarray) -> None:
+        """Key spill of kslots (their full key buffers into the new pages
+        phys, one each) and value spill of vslots (the oldest G values into
+        the value half of their first value-less page) (pipeline.py:183-256).
+        One launch each; one launch for both when R = 0 (the same slots and
+        pages)."""
         G, R = self.config.q_buffer_size, self.config.local_value_window
         both = R == 0
         if len(kslots):
-            phys = [self._alloc(layer, s, seq, 1)[0] for s, seq in zip(kslots.tolist(), seq_ids)]
             pno = self._npages[kslots, layer]
             self._pages[kslots, layer, pno] = phys
             meta = self._h2d(np.stack([kslots, pno, np.asarray(phys)]))   # one copy: slots, page numbers, ids
@@ -319,6 +337,9 @@ class KittyInferencePipeline:
             t = 0
             f = int(self._fill[s, l])
             n_s = min(T, S - f) if f < S else 0
+            # the chunk's new key pages, all or nothing, before any state changes
+            n_full = (int(self._qlen[s, l]) + T - n_s) // G if T > n_s else 0
+            phys = self._alloc_spill(l, np.array([s]), [seq], [n_full]) if n_full else []
             if n_s:
                 self._sink_k[s, l, :, f:f + n_s] = keys[i, :, :n_s]
                 self._sink_v[s, l, :, f:f + n_s] = values[i, :, :n_s]
@@ -329,11 +350,7 @@ class KittyInferencePipeline:
                 # keys: buffered keys + the chunk, cut into full pages and a new buffer
                 nk = int(self._qlen[s, l])
                 kall = torch.cat([self._qbuf_k[s, l, :, :nk], keys[i, :, t:]], dim=1)   # (H, nk + m, D)
-                n_full = (nk + m) // G
                 if n_full:
-                    if self._store is None:
-                        raise RuntimeError("kitty (MI355X build) quantises only on ROCm devices")
-                    phys = self._alloc(l, s, seq, n_full)
                     p0 = int(self._npages[s, l])
                     self._pages[s, l, p0:p0 + n_full] = phys
                     pages = self._h2d(np.asarray(phys))

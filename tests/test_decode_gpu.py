@@ -36,6 +36,8 @@ def _to(dev, *arrs):
     (8, 8, 128, 128, 16, 7, 32, 96),  # config 1 shape: ctx 1024 = 32 + 7*128 + 96
     (2, 16, 128, 128, 32, 3, 7, 0),
     (2, 4, 64, 32, 8, 6, 1, 31),
+    (2, 4, 256, 128, 32, 2, 5, 17),   # generic kernel at the largest head_dim
+    (1, 2, 128, 256, 16, 2, 3, 100),  # and the largest page
 ])
 def test_paged_attention_single_sequence(dev, H, Hq, D, G, dk, n_pages, n_sink, n_tail):
     from kitty.kernels import paged_attention

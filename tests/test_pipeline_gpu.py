@@ -297,3 +297,44 @@ def test_bulk_prefill_matches_token_pushes(dev, D, G, S, pre, T, R):
             for x, y in zip(pa, pb):
                 assert all(torch.equal(u, v) for u, v in zip(x, y))
     assert not a.overflowed() and not b.overflowed()
+
+
+def test_spill_on_full_pool_raises_and_leaves_state_unchanged(dev):
+    """A push whose spill needs more pages than the pool has free raises the
+    reference's exhaustion error (layout.py:161-203) before any state
+    changes: counters, buffers and the free count are as before, the token
+    is not appended, and after another sequence is reset the same push
+    goes through."""
+    cfg = _cfg(num_kv_heads=2, head_dim=16, q_buffer_size=8, sink_size=4, local_value_window=8,
+               max_batch_size=3, pool_pages_override=5)
+    H, D, G, S = cfg.num_kv_heads, cfg.head_dim, cfg.q_buffer_size, cfg.sink_size
+    gen = torch.Generator().manual_seed(21)
+    p, lay, _ = _pipe(cfg)
+    ids = [0, 1, 2]
+    for _ in range(S + G - 1):                   # one token short of the first spill
+        k, v = torch.randn(3, H, D, generator=gen).half(), torch.randn(3, H, D, generator=gen).half()
+        p.push_tokens(0, k, v, ids)
+    k, v = torch.randn(3, H, D, generator=gen).half(), torch.randn(3, H, D, generator=gen).half()
+    p.push_tokens(0, k, v, ids)                  # 3 key spills: 3 of the 5 pages
+    for _ in range(G - 1):
+        k, v = torch.randn(3, H, D, generator=gen).half(), torch.randn(3, H, D, generator=gen).half()
+        p.push_tokens(0, k, v, ids)
+    assert lay.memory_stats()["pages_free"] == 2
+    before = {c: getattr(p, c).copy() for c in ("_fill", "_qlen", "_npages", "_npv", "_vlen")}
+    lens_before = p.lens.clone()
+    k, v = torch.randn(3, H, D, generator=gen).half(), torch.randn(3, H, D, generator=gen).half()
+    with pytest.raises(RuntimeError, match="exhausted"):
+        p.push_tokens(0, k, v, ids)              # needs 3 pages, 2 free
+    torch.cuda.synchronize()
+    assert lay.memory_stats()["pages_free"] == 2
+    for c, a in before.items():
+        assert np.array_equal(getattr(p, c), a), c
+    assert torch.equal(p.lens, lens_before)
+    assert not p.overflowed()
+    p.reset_sequence(2)                          # frees its page: 3 free
+    p.push_tokens(0, k[:2], v[:2], [0, 1])       # two key spills (and two value spills) fit now
+    torch.cuda.synchronize()
+    assert lay.memory_stats()["pages_free"] == 1
+    assert [int(x) for x in p._npages[[p.slot(0), p.slot(1)], 0]] == [2, 2]
+    assert [int(x) for x in p._npv[[p.slot(0), p.slot(1)], 0]] == [1, 1]
+    assert not p.overflowed()

@@ -72,7 +72,8 @@ def test_config2_quantize_pack_bit_exact(dev):
                         Vn[g * G:(g + 1) * G, h].copy(), bi[h].numpy(), Dk, sentinel)
 
 
-@pytest.mark.parametrize("D,G,Dk,H", [(16, 8, 4, 2), (128, 128, 32, 4), (64, 32, 15, 1), (32, 16, 0, 3)])
+@pytest.mark.parametrize("D,G,Dk,H", [(16, 8, 4, 2), (128, 128, 32, 4), (64, 32, 15, 1), (32, 16, 0, 3),
+                                     (256, 128, 32, 2), (128, 256, 16, 1)])   # D*G = 32768: > 64 KB of LDS
 def test_small_shapes_and_edge_rows(dev, D, G, Dk, H):
     from kitty.kernels.ops import quantize_into_pools
     gen = torch.Generator().manual_seed(D * 7 + G)
