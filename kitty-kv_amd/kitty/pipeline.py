@@ -285,40 +285,46 @@ class KittyInferencePipeline:
         phys, one each) and value spill of vslots (the oldest G values into
         the value half of their first value-less page) (pipeline.py:183-256).
         One launch each; one launch for both when R = 0 (the same slots and
-        pages)."""
+        pages).  The host counters are advanced first; their new values for
+        every touched slot travel to the device with the slots and page ids
+        in one pinned copy and land in one indexed write."""
         G, R = self.config.q_buffer_size, self.config.local_value_window
         both = R == 0
-        if len(kslots):
-            pno = self._npages[kslots, layer]
+        k, v = len(kslots), (0 if both else len(vslots))
+        pno = self._npages[kslots, layer].copy()
+        vphys = self._pages[vslots, layer, self._npv[vslots, layer]] if v else np.zeros(0, np.int64)
+        if k:
             self._pages[kslots, layer, pno] = phys
-            meta = self._h2d(np.stack([kslots, pno, np.asarray(phys)]))   # one copy: slots, page numbers, ids
-            sl, pn, pages = meta[0].long(), meta[1].long(), meta[2]
-            kblk = self._qbuf_k[:, layer].index_select(0, sl)             # (n, H, G, D)
-            vblk = self._vbuf[:, layer].index_select(0, sl)[:, :, :G] if both else None
-            quantize_into_pools(self._store, kblk, vblk, self.boost_idx_uint8[layer], pages, self.config.sentinel)
-            self._block_table[layer, sl, pn] = pages
             self._npages[kslots, layer] += 1
             self._qlen[kslots, layer] = 0
-            self.lens[_QLEN, layer, sl] = 0
-            self.lens[_NPAGES, layer, sl] += 1
             if both:
                 self._npv[kslots, layer] += 1
                 self._vlen[kslots, layer] = 0
-                self.lens[_NPAGES_V, layer, sl] += 1
-                self.lens[_VLEN, layer, sl] = 0
-        if len(vslots) and not both:
-            phys = self._pages[vslots, layer, self._npv[vslots, layer]]
-            meta = self._h2d(np.stack([vslots, phys]))
-            sl, pages = meta[0].long(), meta[1]
-            vb = self._vbuf[:, layer]                                     # (slots, H, R + G, D)
-            vblk = vb.index_select(0, sl)                                 # a copy: the shift below may reuse rows
-            quantize_into_pools(self._store, None, vblk[:, :, :G], None, pages, self.config.sentinel)
-            if R:
-                vb[sl, :, :R] = vblk[:, :, G:G + R]                       # the R newest values move to the front
+        if v:
             self._npv[vslots, layer] += 1
             self._vlen[vslots, layer] -= G
-            self.lens[_NPAGES_V, layer, sl] += 1
-            self.lens[_VLEN, layer, sl] -= G
+        touched = np.union1d(kslots, vslots[:v]).astype(np.int64)
+        lens_new = np.stack([c[touched, layer] for c in (self._fill, self._qlen, self._npages, self._npv, self._vlen)])
+        nt = len(touched)
+        meta = self._h2d(np.concatenate([kslots, pno, np.asarray(phys, np.int64), vslots[:v], vphys, touched,
+                                         lens_new.ravel()]))
+        ksl, kpn, kpages = meta[:k].long(), meta[k:2 * k].long(), meta[2 * k:3 * k]
+        o = 3 * k
+        vsl, vpages = meta[o:o + v].long(), meta[o + v:o + 2 * v]
+        o += 2 * v
+        tsl, lens_dev = meta[o:o + nt].long(), meta[o + nt:o + 6 * nt].view(5, nt)
+        if k:
+            kblk = self._qbuf_k[:, layer].index_select(0, ksl)            # (n, H, G, D)
+            vblk = self._vbuf[:, layer].index_select(0, ksl)[:, :, :G] if both else None
+            quantize_into_pools(self._store, kblk, vblk, self.boost_idx_uint8[layer], kpages, self.config.sentinel)
+            self._block_table[layer, ksl, kpn] = kpages
+        if v:
+            vb = self._vbuf[:, layer]                                     # (slots, H, R + G, D)
+            vblk = vb.index_select(0, vsl)                                # a copy: the shift below reuses rows
+            quantize_into_pools(self._store, None, vblk[:, :, :G], None, vpages, self.config.sentinel)
+            if R:
+                vb[vsl, :, :R] = vblk[:, :, G:G + R]                      # the R newest values move to the front
+        self.lens[:, layer, tsl] = lens_dev
 
     # ------------------------------------------------------------ prefill
     def push_chunk(self, layer_id: int, keys: torch.Tensor, values: torch.Tensor, seq_ids: Sequence[int]) -> None:
