@@ -414,8 +414,8 @@ def module_leg(torch, dev, cfg_name: str = "cfg3", cycles: int = 2) -> dict:
             "spill_step_extra_us": round(worst - med, 2),
             "note": "each step: append of all B tokens, key/value spills every G steps (one key-only and one "
                     "value-only batch-quantize launch over B*Hkv blocks plus the value-buffer shift), decode "
-                    "with independent key/value streams (streaming split kernel) and merge; host clock over "
-                    "the timed steps includes the Python module overhead"}
+                    "with independent key/value streams (page-pair split kernel, key-only pages in its FP16 "
+                    "segments) and merge; host clock over the timed steps includes the Python module overhead"}
 
 
 def spill_latency(torch, dev, B: int = 16, Hkv: int = 8, dk: int = 16, reps: int = 64) -> dict:

@@ -6,9 +6,9 @@ namespace kitty {
 
 constexpr int kChunkMax = 256; // tokens per softmax chunk in the generic path (>= G)
 
-// Internal flags bit (not part of the public ABI): run the streaming kernel
-// for a single K/V stream too.  It always runs when the value stream is
-// independent (num_pages_v given), which the page-pair kernel does not take.
+// Internal flags bit (not part of the public ABI): run the streaming split
+// kernel instead of the page-pair one (A/B timing; both take either stream
+// layout).
 constexpr int KITTY_DECODE_STREAM_KERNEL = 1 << 30;
 
 // Waves per SIMD of the streaming kernel for GQA groups of 4 and 8 (its
@@ -84,6 +84,17 @@ __device__ __forceinline__ SeqLens seq_lens(const DecodeParams &p, int b)
     return L;
 }
 
+// Page count the unit plan and the page path see for sequence b: its key
+// pages with one stream, its pages that also hold values (npv) with an
+// independent value stream; -1 (one poisoned unit) for a bad sequence.
+__device__ __forceinline__ int seq_np_raw(const DecodeParams &p, int b)
+{
+    if (!p.num_pages_v)
+        return p.num_pages[b];
+    const SeqLens L = seq_lens(p, b);
+    return L.bad ? -1 : L.npv;
+}
+
 // Partials per (b, query head) of the uniform plan: page splits, then FP16 splits.
 __host__ __device__ inline int num_partials(const DecodeParams &p) { return p.n_splits + p.n_fp16; }
 
@@ -155,7 +166,7 @@ int launch_splits(const DecodeParams &p, hipStream_t stream);
 bool mfma_shape_supported(const DecodeParams &p);
 inline bool uses_stream_kernel(const DecodeParams &p)
 {
-    return (p.flags & KITTY_DECODE_STREAM_KERNEL) || p.num_pages_v;
+    return (p.flags & KITTY_DECODE_STREAM_KERNEL) != 0;
 }
 bool mfma_path_supported(const DecodeParams &p);
 int launch_mfma(const DecodeParams &p, hipStream_t stream);

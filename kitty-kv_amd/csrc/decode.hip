@@ -469,8 +469,9 @@ int launch_generic(const DecodeParams &p, hipStream_t stream)
     return check_launch("decode_generic_kernel");
 }
 
-// Split phase: the MFMA kernel for the production shape, the generic kernel
-// for every other shape the reference accepts.
+// Split phase: the page-pair MFMA kernel for the production shape (the
+// streaming one on request), the generic kernel for every other shape the
+// reference accepts.
 int launch_splits(const DecodeParams &p, hipStream_t stream)
 {
     if (mfma_path_supported(p)) {

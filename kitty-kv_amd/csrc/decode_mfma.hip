@@ -248,137 +248,6 @@ __device__ __forceinline__ void wait_vmcnt()
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Sink + tail tokens [lo, hi) of pair (b, kh) (sink tokens first), 32 per
-// step.  The step's K and V rows stream into the two LDS stages with
-// global_load_lds (no registers hold data in flight): K chunk c of token row n
-// is stored at chunk c ^ (n & 15), so the 16 rows one MFMA B read touches hit
-// 16 different bank groups.  QK: f16 MFMAs with the heads on rows (A = q,
-// B = K rows, exact products; scores times sm_scale log2(e) in fp32), base-2
-// online softmax per head row
-// with DPP row reductions, P through LDS.  PV: VALU, lane = channel pair.
-// Returns each head's (m, l) and O (channels 2 lane, 2 lane + 1).
-template <int GQ>
-__device__ void fp16_segments(const DecodeParams &p, int b, int kh, int lo, int hi, unsigned char *kst,
-                              unsigned char *vst, float *m_out, float *l_out, float (*O)[2])
-{
-    constexpr int kTok = 32;
-    const int lane = threadIdx.x, r = lane & 15, kq = lane >> 4;
-    float *pbuf = (float *)(vst + kTok * 256);  // [head][token] fp32, GQ * 32 floats
-    // A operand: row r = head r (rows past GQ are zero), k = 8 kq + i of each
-    // 32-channel step
-    // (fp16 q as is: q k is exact in the fp32 accumulator, and the scores
-    // are scaled by sm_scale log2(e) afterwards)
-    half8 qa[4];
-    const float qk_c = p.sm_scale * kLog2e;
-    {
-        const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + (r < GQ ? r : 0)) * p.q_s_head;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const u32x4 raw = *(const u32x4 *)(qrow + 32 * s + 8 * kq);
-            u32x4 v;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                v[j] = r < GQ ? raw[j] : 0u;
-            qa[s] = __builtin_bit_cast(half8, v);
-        }
-    }
-    float m[4], l[4];  // head rows 4 kq + i
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        m[i] = -__builtin_inff();
-        l[i] = 0.0f;
-    }
-#pragma unroll
-    for (int g = 0; g < GQ; ++g)
-        O[g][0] = O[g][1] = 0.0f;
-    const int ns = min(max(0, p.sink_len[b]), p.sink_cap);
-    const uint16_t *sk = p.sink_k.ptr + b * p.sink_k.s_seq + kh * p.sink_k.s_head;
-    const uint16_t *sv = p.sink_v.ptr + b * p.sink_v.s_seq + kh * p.sink_v.s_head;
-    const uint16_t *tk = p.tail_k.ptr + b * p.tail_k.s_seq + kh * p.tail_k.s_head;
-    const uint16_t *tv = p.tail_v.ptr + b * p.tail_v.s_seq + kh * p.tail_v.s_head;
-    for (int c0 = lo; c0 < hi; c0 += kTok) {
-        const int cnt = min(kTok, hi - c0);
-        // ---- 16 direct-to-LDS loads: instruction i covers rows 4i .. 4i+3
-#pragma unroll
-        for (int i = 0; i < kTok / 4; ++i) {
-            const int n = 4 * i + kq;                 // token row of this lane's slot
-            const int tt = c0 + min(n, cnt - 1);      // rows past cnt repeat the last token
-            const bool sink = tt < ns;
-            const uint16_t *krow = sink ? sk + (int64_t)tt * p.sink_k.s_tok : tk + (int64_t)(tt - ns) * p.tail_k.s_tok;
-            const uint16_t *vrow = sink ? sv + (int64_t)tt * p.sink_v.s_tok : tv + (int64_t)(tt - ns) * p.tail_v.s_tok;
-            gll16((const unsigned char *)(krow + 8 * (r ^ (n & 15))), kst + 1024 * i);
-            gll16((const unsigned char *)(vrow + 8 * r), vst + 1024 * i);
-        }
-        wait_vmcnt<0>();
-        // ---- QK: tile tg covers tokens 16 tg + r; S[tg][i] = head 4 kq + i
-        f32x4 S[2];
-#pragma unroll
-        for (int tg = 0; tg < 2; ++tg) {
-            S[tg] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            const int n = 16 * tg + r;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const half8 kb = *(const half8 *)(kst + 256 * n + 16 * ((4 * s + kq) ^ r));
-                S[tg] = mfma(qa[s], kb, S[tg]);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                S[tg][i] *= qk_c;
-        }
-        // ---- online softmax per head row (tokens past cnt masked)
-        float alpha[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float s0 = r < cnt ? S[0][i] : -__builtin_inff();
-            const float s1 = 16 + r < cnt ? S[1][i] : -__builtin_inff();
-            const float mx = row_max16(fmaxf(s0, s1));
-            const float mn = fmaxf(m[i], mx);
-            alpha[i] = __builtin_amdgcn_exp2f(m[i] - mn);
-            const float p0 = __builtin_amdgcn_exp2f(s0 - mn), p1 = __builtin_amdgcn_exp2f(s1 - mn);
-            l[i] = l[i] * alpha[i] + row_sum16(p0 + p1);
-            m[i] = mn;
-            const int h = 4 * kq + i;
-            if (h < GQ) {
-                pbuf[h * kTok + r] = p0;
-                pbuf[h * kTok + 16 + r] = p1;
-            }
-        }
-        __syncthreads();
-        // ---- PV: lane = channels 2 lane, 2 lane + 1
-#pragma unroll
-        for (int g = 0; g < GQ; ++g) {
-            const float al = __builtin_bit_cast(
-                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha[g & 3]), 16 * (g >> 2)));
-            O[g][0] *= al;
-            O[g][1] *= al;
-        }
-#pragma unroll
-        for (int t4 = 0; t4 < kTok / 4; ++t4) {
-            unsigned vv[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                vv[e] = *(const unsigned *)(vst + 256 * (4 * t4 + e) + 4 * lane);
-#pragma unroll
-            for (int g = 0; g < GQ; ++g) {
-                const float4 w = *(const float4 *)(pbuf + g * kTok + 4 * t4);
-                const float wt[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const half2v h = as_h2(vv[e]);
-                    O[g][0] += wt[e] * (float)h[0];
-                    O[g][1] += wt[e] * (float)h[1];
-                }
-            }
-        }
-        __syncthreads();  // LDS reads done before the next step's loads land
-    }
-#pragma unroll
-    for (int g = 0; g < GQ; ++g) {
-        m_out[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m[g & 3]), 16 * (g >> 2)));
-        l_out[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l[g & 3]), 16 * (g >> 2)));
-    }
-}
-
 // Running state of one wave across its pages.
 template <int GQ>
 struct WaveState {
@@ -512,12 +381,15 @@ __device__ __forceinline__ void pv_fp8_fp4(WaveState<GQ> &W, unsigned char *st, 
 }
 
 // One (page, head) record in LDS stage `st` -> QK, online softmax, PV.
+// QK of the (page, head) record in stage `st`: S[cb][a] holds 4^a 2^-24
+// sum_k A c for tokens 64 cb + 4 r + a on the head rows (rounded product and
+// residual rows, or one row and a second chain at GQA 16), Yt the
+// zero-point term Y per head row.
 template <int GQ>
-__device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st, int lane, int Dk)
+__device__ __forceinline__ void page_qk(const WaveState<GQ> &W, const unsigned char *st, int lane, int Dk,
+                                        f32x4 (&S)[2][4], f32x4 &Yt)
 {
-    constexpr int HPL = GQ / 4;
-    constexpr int RSTEP = 4 / HPL;  // accumulator register of head slot j = j * RSTEP
-    const int q = lane >> 4, r = lane & 15;
+    const int q = lane >> 4;
 
     // ---------------- operands from LDS, issued together
     u32x4 ks[4], kz[4];
@@ -546,7 +418,7 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     // and the bias tile Y = sum A z (per head row, broadcast over token
     // columns)
     half8 A[4], Ahi, Al[4], Alhi;
-    f32x4 Yt = {0.0f, 0.0f, 0.0f, 0.0f};
+    Yt = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         u32x4 av;
@@ -591,7 +463,6 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     // ---------------- QK token tiles: S[cb][a] covers tokens 64cb + 4r + a.
     // S[cb][a] ends at 4^a 2^-24 sum_k A c; the softmax scales it back and
     // subtracts the zero-point term Y.
-    f32x4 S[2][4];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
         S[0][a] = S[1][a] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -623,6 +494,16 @@ __device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st
     }
 
     __builtin_amdgcn_s_setprio(0);
+}
+
+template <int GQ>
+__device__ __forceinline__ void compute_page(WaveState<GQ> &W, unsigned char *st, int lane, int Dk)
+{
+    constexpr int HPL = GQ / 4;
+    constexpr int RSTEP = 4 / HPL;  // accumulator register of head slot j = j * RSTEP
+    const int q = lane >> 4, r = lane & 15;
+    f32x4 S[2][4], Yt;
+    page_qk<GQ>(W, st, lane, Dk, S, Yt);
     if constexpr (GQ == 4) {
         pv_fp8_fp4(W, st, S, Yt, lane);
         return;
@@ -758,44 +639,25 @@ __device__ __forceinline__ SegSetup load_setup(const DecodeParams &p, int b, int
     return s;
 }
 
-// Pages [p0, p1) of pair (b, kh) folded into partial t: row t * GQ + h
-// holds query head kh * GQ + h.  A page count outside [0, max_pages] or a
-// page id outside the pool makes the partial NaN; no pages leave an empty
-// partial (m = -inf, l = 0, O = 0).
+// QK operand state of pair (b, kh) for its pages (page_qk): the static fp16
+// q halves, the high-bit rows' q values and channels, the tr8 offsets and
+// the score scale.  scratch: LDS the wave may overwrite (256 + GQ * 256 B),
+// free again on return.
 template <int GQ>
-__device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned char *stage0, unsigned char *stage1,
-                                             int b, int kh, int np_raw, int p0, int p1, int64_t t, const SegSetup &su)
+__device__ __forceinline__ void qk_setup(WaveState<GQ> &W, const DecodeParams &p, int b, int kh, const SegSetup &su,
+                                         unsigned char *scratch, int lane, int Dk)
 {
-    constexpr int HPL = GQ / 4;
-    constexpr int RSTEP = 4 / HPL;
     constexpr int ROWS_PER_HEAD = 16 / GQ;
-    // lane-derived offsets are rebuilt per segment (the asm hides the lane
-    // id): kept across the caller's segment loop they would be spilled
-    int lane = threadIdx.x;
-    asm volatile("" : "+v"(lane));
     const int q = lane >> 4, r = lane & 15;
-    const int Dk = p.Dk;
-    // segment bounds come out of VALU divisions: keep the loop control scalar
-    b = __builtin_amdgcn_readfirstlane(b);
-    kh = __builtin_amdgcn_readfirstlane(kh);
-    np_raw = __builtin_amdgcn_readfirstlane(np_raw);
-    p0 = __builtin_amdgcn_readfirstlane(p0);
-    p1 = __builtin_amdgcn_readfirstlane(p1);
-    bool poison = np_raw < 0 || np_raw > p.max_pages;
-    if (poison)
-        p1 = p0;
-    else if (p1 > np_raw)
-        p1 = np_raw;
-
     // rank -> channel map of this KV head (inverse of boost_idx) and the q
-    // rows of the group, staged in stage1 before any page lands there; the
+    // rows of the group, staged in scratch before any page lands there; the
     // boosted channels' q values are then read from LDS, not by a global load
     // that would wait on the map (one memory round trip before the first
     // page's loads).
     const bool head_row = (r % ROWS_PER_HEAD) == 0;
     const int hr = r / ROWS_PER_HEAD;  // head of MFMA row r
-    int *rank_chan = (int *)stage1;
-    _Float16 *q_lds = (_Float16 *)(stage1 + 256);  // [GQ][128]
+    int *rank_chan = (int *)scratch;
+    _Float16 *q_lds = (_Float16 *)(scratch + 256);  // [GQ][128]
     if (lane < 32)
         rank_chan[lane] = 0;
     __syncthreads();
@@ -811,7 +673,6 @@ __device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned cha
 
     __syncthreads();
 
-    WaveState<GQ> W;
     // Static half of the QK A operand: the fp16 q of the lane's 8 channels
     // of every K-step on the two rows of each head (the product with the key
     // scale and its residual, qk_residual), zero on the other rows.
@@ -852,6 +713,39 @@ __device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned cha
         W.tr_base0 = 32 * tr_row + 16 * (0 ^ (q & 1)) + 8 * (r & 1);
         W.tr_base1 = 32 * tr_row + 16 * (1 ^ (q & 1)) + 8 * (r & 1);
     }
+}
+
+// Pages [p0, p1) of pair (b, kh) folded into partial t: row t * GQ + h
+// holds query head kh * GQ + h.  A page count outside [0, max_pages] or a
+// page id outside the pool makes the partial NaN; no pages leave an empty
+// partial (m = -inf, l = 0, O = 0).
+template <int GQ>
+__device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned char *stage0, unsigned char *stage1,
+                                             int b, int kh, int np_raw, int p0, int p1, int64_t t, const SegSetup &su)
+{
+    constexpr int HPL = GQ / 4;
+    constexpr int RSTEP = 4 / HPL;
+    constexpr int ROWS_PER_HEAD = 16 / GQ;
+    // lane-derived offsets are rebuilt per segment (the asm hides the lane
+    // id): kept across the caller's segment loop they would be spilled
+    int lane = threadIdx.x;
+    asm volatile("" : "+v"(lane));
+    const int q = lane >> 4, r = lane & 15;
+    const int Dk = p.Dk;
+    // segment bounds come out of VALU divisions: keep the loop control scalar
+    b = __builtin_amdgcn_readfirstlane(b);
+    kh = __builtin_amdgcn_readfirstlane(kh);
+    np_raw = __builtin_amdgcn_readfirstlane(np_raw);
+    p0 = __builtin_amdgcn_readfirstlane(p0);
+    p1 = __builtin_amdgcn_readfirstlane(p1);
+    bool poison = np_raw < 0 || np_raw > p.max_pages;
+    if (poison)
+        p1 = p0;
+    else if (p1 > np_raw)
+        p1 = np_raw;
+
+    WaveState<GQ> W;
+    qk_setup<GQ>(W, p, b, kh, su, stage1, lane, Dk);
     // tr4 offsets of value rows R = 32q + 16k + r (GQA 4): 16-byte chunk c of
     // row R sits at 32 R + 16 (c ^ ((R >> 3) & 1)) in the stage.
 #pragma unroll
@@ -1015,9 +909,12 @@ __device__ __forceinline__ int64_t uniform64(int64_t v)
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// FP16-region tokens of sequence b: sinks and the value tail (the key-only
+// pages' tokens and the key tail); none for a bad sequence.
 __device__ __forceinline__ int seq_tokens(const DecodeParams &p, int b)
 {
-    return min(max(0, p.sink_len[b]), p.sink_cap) + min(max(0, p.tail_len[b]), p.tail_cap);
+    const SeqLens L = seq_lens(p, b);
+    return L.ns + L.nv;
 }
 
 // Sequence b as the unit plan sees it (all fields wave-uniform).
@@ -1057,6 +954,214 @@ __device__ __forceinline__ DecodeParams kernel_params(KernargParams pp)
     __builtin_memcpy(&r, (const void *)pp, sizeof(r));
     return r;
 }
+
+// FP16-region tokens [lo, hi) of pair (b, kh), 32 per step.  The region is
+// the sinks, then the tokens of the key-only pages P_v .. P_k - 1 (an
+// independent value stream: their keys are quantised, their values are the
+// first (P_k - P_v) G rows of the value tail), then the key tail, whose
+// values follow in the value tail; with one stream the middle part is empty.
+// A step's rows stream into the two LDS stages with global_load_lds (no
+// registers hold data in flight): K chunk c of token row n is stored at
+// chunk c ^ (n & 15), so the 16 rows one MFMA B read touches hit 16
+// different bank groups.  QK: f16 MFMAs with the heads on rows (A = q,
+// B = K rows, exact products; scores times sm_scale log2(e) in fp32); for a
+// key-only page the page path's exact QK (page_qk) writes the page's scores
+// to kst once and its steps read them back.  Base-2 online softmax per head
+// row with DPP row reductions, P through LDS.  PV: VALU, lane = channel
+// pair.  Steps do not cross from sinks into key-only pages, nor out of one.
+// Returns each head's (m, l) and O (channels 2 lane, 2 lane + 1); m is NaN
+// if a key-only page id lies outside the pool.
+template <int GQ>
+__device__ void fp16_segments(const DecodeParams &p, int b, int kh, int lo, int hi, unsigned char *kst,
+                              unsigned char *vst, float *m_out, float *l_out, float (*O)[2])
+{
+    constexpr int kTok = 32;
+    constexpr int HPL = GQ / 4;
+    constexpr int RSTEP = 4 / HPL;
+    const int lane = threadIdx.x, r = lane & 15, kq = lane >> 4;
+    float *pbuf = (float *)(vst + kTok * 256);  // [head][token] fp32, GQ * 32 floats
+    // A operand: row r = head r (rows past GQ are zero), k = 8 kq + i of each
+    // 32-channel step
+    // (fp16 q as is: q k is exact in the fp32 accumulator, and the scores
+    // are scaled by sm_scale log2(e) afterwards)
+    half8 qa[4];
+    const float qk_c = p.sm_scale * kLog2e;
+    {
+        const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + (r < GQ ? r : 0)) * p.q_s_head;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const u32x4 raw = *(const u32x4 *)(qrow + 32 * s + 8 * kq);
+            u32x4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                v[j] = r < GQ ? raw[j] : 0u;
+            qa[s] = __builtin_bit_cast(half8, v);
+        }
+    }
+    float m[4], l[4];  // head rows 4 kq + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m[i] = -__builtin_inff();
+        l[i] = 0.0f;
+    }
+#pragma unroll
+    for (int g = 0; g < GQ; ++g)
+        O[g][0] = O[g][1] = 0.0f;
+    const SeqLens L = seq_lens(p, b);
+    const int ns = L.ns, kbeg = L.ns, kend = L.ns + L.nmix;  // key-only tokens [kbeg, kend)
+    const uint16_t *sk = p.sink_k.ptr + b * p.sink_k.s_seq + kh * p.sink_k.s_head;
+    const uint16_t *sv = p.sink_v.ptr + b * p.sink_v.s_seq + kh * p.sink_v.s_head;
+    const uint16_t *tk = p.tail_k.ptr + b * p.tail_k.s_seq + kh * p.tail_k.s_head;
+    const uint16_t *tv = p.tail_v.ptr + b * p.tail_v.s_seq + kh * p.tail_v.s_head;
+    const float *sc = (const float *)kst;  // [GQ][128] scores of the key-only page in hand
+    int page_in_kst = -1;
+    bool poison = false;
+    for (int c0 = lo; c0 < hi;) {
+        int end = min(hi, c0 + kTok);
+        const bool konly = c0 >= kbeg && c0 < kend;
+        const int pg = konly ? (c0 - kbeg) >> 7 : 0;  // key-only page of this step
+        if (konly)
+            end = min(end, kbeg + 128 * (pg + 1));
+        else if (c0 < kbeg && kend > kbeg)
+            end = min(end, kbeg);
+        const int cnt = end - c0;
+        f32x4 S[2];
+        if (konly) {
+            if (pg != page_in_kst) {
+                // scores of key page P_v + pg: the page path's QK into kst
+                const int32_t page = p.block_table[(int64_t)b * p.bt_stride + L.npv + pg];
+                if (page < 0 || page >= p.num_pool_pages) {
+                    poison = true;
+                    c0 = min(hi, kbeg + 128 * (pg + 1));
+                    continue;
+                }
+                WaveState<GQ> W;
+                const SegSetup su = load_setup<GQ>(p, b, kh, L.npv + pg, L.npv + pg + 1);
+                qk_setup<GQ>(W, p, b, kh, su, vst, lane, p.Dk);
+                issue_page(kst, page_src(p, (int64_t)page * p.Hkv + kh), lane, p.Dk);
+                wait_vmcnt<0>();
+                f32x4 Sp[2][4], Yt;
+                page_qk<GQ>(W, kst, lane, p.Dk, Sp, Yt);
+                const int q = kq;
+                float *scw = (float *)kst;
+#pragma unroll
+                for (int j = 0; j < HPL; ++j) {
+                    const int ri = j * RSTEP;
+                    const float yk = (GQ == 16 ? Yt[ri] : Yt[ri] + Yt[ri + 1]) * qk_c;
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                        for (int a = 0; a < 4; ++a)
+                            scw[(q * HPL + j) * 128 + 64 * cb + 4 * r + a] =
+                                (GQ == 16 ? Sp[cb][a][ri] : Sp[cb][a][ri] + Sp[cb][a][ri + 1]) *
+                                    (qk_c * (kSub / (float)(1 << (2 * a)))) - yk;
+                }
+                __syncthreads();  // scores in kst before they are read back
+                page_in_kst = pg;
+            }
+            // ---- value rows of the step: value-tail rows c0 - ns ..
+#pragma unroll
+            for (int i = 0; i < kTok / 4; ++i) {
+                const int n = 4 * i + kq;
+                const int tt = c0 + min(n, cnt - 1);
+                gll16((const unsigned char *)(tv + (int64_t)(tt - ns) * p.tail_v.s_tok + 8 * r), vst + 1024 * i);
+            }
+            wait_vmcnt<0>();
+            const int t0 = c0 - kbeg - 128 * pg;  // page token of the step's first token
+#pragma unroll
+            for (int tg = 0; tg < 2; ++tg)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int h = 4 * kq + i, t = 16 * tg + r;
+                    S[tg][i] = h < GQ && t < cnt ? sc[h * 128 + t0 + t] : 0.0f;
+                }
+        } else {
+            // ---- 16 direct-to-LDS loads: instruction i covers rows 4i .. 4i+3
+#pragma unroll
+            for (int i = 0; i < kTok / 4; ++i) {
+                const int n = 4 * i + kq;                 // token row of this lane's slot
+                const int tt = c0 + min(n, cnt - 1);      // rows past cnt repeat the last token
+                const bool sink = tt < ns;
+                const uint16_t *krow = sink ? sk + (int64_t)tt * p.sink_k.s_tok
+                                            : tk + (int64_t)(tt - kend) * p.tail_k.s_tok;
+                const uint16_t *vrow = sink ? sv + (int64_t)tt * p.sink_v.s_tok
+                                            : tv + (int64_t)(tt - ns) * p.tail_v.s_tok;
+                gll16((const unsigned char *)(krow + 8 * (r ^ (n & 15))), kst + 1024 * i);
+                gll16((const unsigned char *)(vrow + 8 * r), vst + 1024 * i);
+            }
+            wait_vmcnt<0>();
+            // ---- QK: tile tg covers tokens 16 tg + r; S[tg][i] = head 4 kq + i
+#pragma unroll
+            for (int tg = 0; tg < 2; ++tg) {
+                S[tg] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                const int n = 16 * tg + r;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const half8 kb = *(const half8 *)(kst + 256 * n + 16 * ((4 * s + kq) ^ r));
+                    S[tg] = mfma(qa[s], kb, S[tg]);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    S[tg][i] *= qk_c;
+            }
+            page_in_kst = -1;  // K rows went over any page scores
+        }
+        // ---- online softmax per head row (tokens past cnt masked)
+        float alpha[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float s0 = r < cnt ? S[0][i] : -__builtin_inff();
+            const float s1 = 16 + r < cnt ? S[1][i] : -__builtin_inff();
+            const float mx = row_max16(fmaxf(s0, s1));
+            const float mn = fmaxf(m[i], mx);
+            alpha[i] = __builtin_amdgcn_exp2f(m[i] - mn);
+            const float p0 = __builtin_amdgcn_exp2f(s0 - mn), p1 = __builtin_amdgcn_exp2f(s1 - mn);
+            l[i] = l[i] * alpha[i] + row_sum16(p0 + p1);
+            m[i] = mn;
+            const int h = 4 * kq + i;
+            if (h < GQ) {
+                pbuf[h * kTok + r] = p0;
+                pbuf[h * kTok + 16 + r] = p1;
+            }
+        }
+        __syncthreads();
+        // ---- PV: lane = channels 2 lane, 2 lane + 1
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+            const float al = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha[g & 3]), 16 * (g >> 2)));
+            O[g][0] *= al;
+            O[g][1] *= al;
+        }
+#pragma unroll
+        for (int t4 = 0; t4 < kTok / 4; ++t4) {
+            unsigned vv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                vv[e] = *(const unsigned *)(vst + 256 * (4 * t4 + e) + 4 * lane);
+#pragma unroll
+            for (int g = 0; g < GQ; ++g) {
+                const float4 w = *(const float4 *)(pbuf + g * kTok + 4 * t4);
+                const float wt[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const half2v h = as_h2(vv[e]);
+                    O[g][0] += wt[e] * (float)h[0];
+                    O[g][1] += wt[e] * (float)h[1];
+                }
+            }
+        }
+        __syncthreads();  // LDS reads done before the next step's loads land
+        c0 = end;
+    }
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+        m_out[g] = poison ? __builtin_nanf("")
+                          : __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m[g & 3]), 16 * (g >> 2)));
+        l_out[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l[g & 3]), 16 * (g >> 2)));
+    }
+}
+
 
 // FP16 tokens [lo, hi) of pair (b, kh) as partial t.  Out of line: the page
 // loop's registers need not be kept around it.
@@ -1111,7 +1216,7 @@ void decode_mfma_kernel(DecodeParams p)
     int np_l = 0, units_l = 0;  // sequence b0 + lane of the current step
     auto load_step = [&](int b0) {
         const int b = b0 + lane;
-        np_l = b < p.B ? p.num_pages[b] : 0;
+        np_l = b < p.B ? seq_np_raw(p, b) : 0;
         units_l = b < p.B ? seq_page_units(np_l, p.max_pages, F) + F : 0;
     };
     load_step(0);
@@ -1154,7 +1259,7 @@ void decode_mfma_kernel(DecodeParams p)
         u_last = uniform64(s1);
         sq.b = g_b;
         sq.base = (int64_t)g_b * p.Hkv * units_s;
-        sq.np_raw = p.B <= 64 ? __builtin_amdgcn_readlane(np_l, g_b) : p.num_pages[g_b];
+        sq.np_raw = p.B <= 64 ? __builtin_amdgcn_readlane(np_l, g_b) : seq_np_raw(p, g_b);
         sq.npu = seq_page_units(sq.np_raw, p.max_pages, F);
     } else {
         // ---- plan for U: prefix sums of the units, 64 sequences per step
@@ -1239,7 +1344,7 @@ void decode_mfma_kernel(DecodeParams p)
             const DecodeParams P = kernel_params(kp);
             sq.b += 1;
             sq.base += Hkv * per_pair;
-            sq.np_raw = P.num_pages[sq.b];
+            sq.np_raw = seq_np_raw(P, sq.b);
             sq.npu = seq_page_units(sq.np_raw, P.max_pages, F);
         }
     }
