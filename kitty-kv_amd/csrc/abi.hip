@@ -15,9 +15,8 @@ void set_error(const std::string &msg) { g_last_error = msg; }
 const char *get_error() { return g_last_error.c_str(); }
 
 // Waves of the decode kernels resident on the current device at once:
-// waves_per_cu per CU (streaming kernel: 4 * KITTY_STREAM_WAVES_PER_EU for
-// GQA groups of 4 and 8, 8 for 16; page-pair MFMA kernel: 8 and 4), 3072 /
-// 2048 on an MI355X.
+// waves_per_cu per CU (MFMA kernel: 8 for GQA groups of 4 and 8, with 20 KB
+// of LDS and up to 256 registers each, 4 for 16), 2048 / 1024 on an MI355X.
 static int64_t resident_waves(int waves_per_cu = 8)
 {
     int dev = 0, cus = 0;
@@ -78,8 +77,7 @@ static void set_plan(DecodeParams &p, const kitty_decode_args &a, bool balanced)
     p.pages_per_split = p.n_splits = 0;
     p.fp16_weight = fp16_weight(p.GQ);
     p.fp16_units = seq_fp16_units(p.sink_cap + p.tail_v_cap, p.fp16_weight);
-    const bool stream = uses_stream_kernel(p);
-    const int64_t res = resident_waves(stream ? (p.GQ <= 8 ? 4 * KITTY_STREAM_WAVES_PER_EU : 8) : (p.GQ <= 8 ? 8 : 4));
+    const int64_t res = resident_waves(p.GQ <= 8 ? 8 : 4);
     if (a.pages_per_split > 0) {
         p.min_chunk = a.pages_per_split;
         const int64_t pairs = (int64_t)a.batch * a.num_kv_heads;
@@ -190,17 +188,12 @@ extern "C" int kitty_decode_workspace_size(const kitty_decode_args *args, size_t
         return rc;
     if (!bytes)
         return fail(KITTY_E_INVALID, "bytes is NULL");
-    // the size must not depend on which kernel the real pointers select:
-    // the largest of the uniform plan and the unit-balanced plans of both
-    // MFMA kernels
+    // the size must not depend on which kernel the real pointers select
     size_t n = workspace_bytes(p);
     if (mfma_shape_supported(p)) {
-        for (int k = 0; k < 3; ++k) {
-            DecodeParams o = p;
-            o.flags = k == 2 ? (p.flags | KITTY_DECODE_STREAM_KERNEL) : (p.flags & ~KITTY_DECODE_STREAM_KERNEL);
-            set_plan(o, *args, k != 0);
-            n = std::max(n, workspace_bytes(o));
-        }
+        DecodeParams o = p;
+        set_plan(o, *args, !p.balanced);
+        n = std::max(n, workspace_bytes(o));
     }
     *bytes = n;
     return KITTY_OK;

@@ -6,18 +6,6 @@ namespace kitty {
 
 constexpr int kChunkMax = 256; // tokens per softmax chunk in the generic path (>= G)
 
-// Internal flags bit (not part of the public ABI): run the streaming split
-// kernel instead of the page-pair one (A/B timing; both take either stream
-// layout).
-constexpr int KITTY_DECODE_STREAM_KERNEL = 1 << 30;
-
-// Waves per SIMD of the streaming kernel for GQA groups of 4 and 8 (its
-// occupancy and register budget; the work plan sizes its grid with it).
-// Three (168 registers, 12 waves and 120 KB of LDS per CU) measured faster
-// than four (128 registers, which spill): 67 vs 78 us at config 3.
-#ifndef KITTY_STREAM_WAVES_PER_EU
-#define KITTY_STREAM_WAVES_PER_EU 3
-#endif
 constexpr int kMaxPagesPerSplit = 64;
 
 struct DecodeParams {
@@ -164,13 +152,8 @@ size_t generic_lds_bytes(int GQ, int D, int G, int Dk);
 int launch_generic(const DecodeParams &p, hipStream_t stream);
 int launch_splits(const DecodeParams &p, hipStream_t stream);
 bool mfma_shape_supported(const DecodeParams &p);
-inline bool uses_stream_kernel(const DecodeParams &p)
-{
-    return (p.flags & KITTY_DECODE_STREAM_KERNEL) != 0;
-}
 bool mfma_path_supported(const DecodeParams &p);
 int launch_mfma(const DecodeParams &p, hipStream_t stream);
-int launch_stream(const DecodeParams &p, hipStream_t stream);
 int launch_merge(const DecodeParams &p, hipStream_t stream);
 
 } // namespace kitty

@@ -469,14 +469,11 @@ int launch_generic(const DecodeParams &p, hipStream_t stream)
     return check_launch("decode_generic_kernel");
 }
 
-// Split phase: the page-pair MFMA kernel for the production shape (the
-// streaming one on request), the generic kernel for every other shape the
-// reference accepts.
+// Split phase: the MFMA kernel for the production shape, the generic kernel
+// for every other shape the reference accepts.
 int launch_splits(const DecodeParams &p, hipStream_t stream)
 {
     if (mfma_path_supported(p)) {
-        if (uses_stream_kernel(p))
-            return launch_stream(p, stream);
         return launch_mfma(p, stream);
     }
     return launch_generic(p, stream);

@@ -1,5 +1,4 @@
-// Exact QK operand of the MFMA decode kernels (shared by decode_mfma.hip
-// and decode_stream.hip).
+// Exact QK operand of the MFMA decode kernel (decode_mfma.hip).
 #pragma once
 #include <cstdint>
 

@@ -26,7 +26,6 @@ KITTY_E_UNSUPPORTED = -3
 KITTY_E_EXHAUSTED = -4
 KITTY_E_NOT_FOUND = -5
 KITTY_DECODE_UNIQUE_BOOST_ROWS = 1
-KITTY_DECODE_STREAM_KERNEL = 1 << 30  # internal: the streaming split kernel for a single K/V stream too
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32

@@ -165,9 +165,6 @@ class DecodePlan:
     value-tail tokens in tail_v (B, Hkv, Tv, D), with
     (num_pages - num_pages_v) * G + tail_len == tail_len_v per sequence.
     Without them both streams use num_pages and tail_len.
-    stream_kernel runs the streaming split kernel (the one that serves an
-    independent value stream) for a single K/V stream too, for A/B timing
-    against the page-pair kernel.
     """
 
     def __init__(self, q: torch.Tensor, block_table: torch.Tensor, num_pages: torch.Tensor,
@@ -178,8 +175,7 @@ class DecodePlan:
                  max_pages: Optional[int] = None, pages_per_split: int = 0,
                  sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
                  workspace: Optional[torch.Tensor] = None, boost_unique: Optional[bool] = None,
-                 num_pages_v: Optional[torch.Tensor] = None, tail_len_v: Optional[torch.Tensor] = None,
-                 stream_kernel: bool = False):
+                 num_pages_v: Optional[torch.Tensor] = None, tail_len_v: Optional[torch.Tensor] = None):
         dev = _hip.require_device(q, block_table, num_pages, key_baseline, key_boost, key_meta, value_pool,
                                   value_meta, boost_idx, sink_k, sink_v, sink_len, tail_k, tail_v, tail_len)
         _need((num_pages_v is None) == (tail_len_v is None), "num_pages_v and tail_len_v go together")
@@ -233,8 +229,7 @@ class DecodePlan:
         a.max_pages, a.pages_per_split = int(max_pages), int(pages_per_split)
         if boost_unique is None:
             boost_unique = boost_rows_unique(boost_idx, key_boost.shape[2])
-        a.flags = (_hip.KITTY_DECODE_UNIQUE_BOOST_ROWS if boost_unique else 0) | \
-            (_hip.KITTY_DECODE_STREAM_KERNEL if stream_kernel else 0)
+        a.flags = _hip.KITTY_DECODE_UNIQUE_BOOST_ROWS if boost_unique else 0
         a.sm_scale = float(1.0 / math.sqrt(D) if sm_scale is None else sm_scale)
         self._L = _hip.load()
         need = ctypes.c_size_t(0)

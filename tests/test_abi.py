@@ -57,12 +57,12 @@ def test_workspace_size_formula():
     from kitty.kernels.ops import decode_workspace_bytes
     row = (128 + 2) * 4  # O + (m, l) per partial row, fp32
     # Config 3 shape on 256 CUs.  Uniform plan (generic kernel): 15 splits of
-    # 17 pages + 1 FP16 split per (b, q head).  Unit-balanced plan (streaming
-    # kernel, 12 waves per CU): GQ rows per partial t < 2 (3072 resident waves
+    # 17 pages + 1 FP16 split per (b, q head).  Unit-balanced plan (MFMA
+    # kernel, 8 waves per CU): GQ rows per partial t < 2 (2048 resident waves
     # + 128 pairs), plus the (first, last) partial table of the pairs.  The
     # size covers both.
     uniform = 16 * 32 * 16 * row
-    balanced = 2 * (3072 + 128) * 4 * row + 128 * 2 * 4
+    balanced = 2 * (2048 + 128) * 4 * row + 128 * 2 * 4
     assert decode_workspace_bytes(16, 32, 8, 128, 128, 16, 255) == max(uniform, balanced)
     # pages_per_split = 200: uniform splits capped at 64 pages (4 + 1 per
     # head); balanced: at least 200 units per wave, 128 pairs x ceil(256 / 200)

@@ -277,19 +277,16 @@ def test_config4_ragged_batch_64bit_offsets(dev):
         _close(out[b], ref, f"config4 b={b} ctx={ctx[b]}")
 
 
-@pytest.mark.parametrize("kernel,Hq,H,D,G,dk", [("page_pair", 32, 8, 128, 128, 16), ("page_pair", 64, 8, 128, 128, 32),
-                                               ("page_pair", 128, 8, 128, 128, 16),
-                                               ("stream", 32, 8, 128, 128, 16), ("stream", 64, 8, 128, 128, 32),
-                                               ("generic", 8, 4, 64, 32, 8)])
+@pytest.mark.parametrize("kernel,Hq,H,D,G,dk", [("mfma", 32, 8, 128, 128, 16), ("mfma", 64, 8, 128, 128, 32),
+                                               ("mfma", 128, 8, 128, 128, 16), ("generic", 8, 4, 64, 32, 8)])
 def test_independent_value_stream(dev, kernel, Hq, H, D, G, dk):
     """Key and value streams of different page counts (P_v <= P_k, the value
     local window of the pipeline): the value rows of key pages P_v..P_k-1 and
     of the key tail come from tail_v, (P_k - P_v) G + tail_len rows of it.
     Against the oracle's split-stream decode, per sequence and head, with
     P_v = P_k (the reference layout), P_v = P_k - 1 (a 128-token window),
-    P_v = 0 (every value FP16) and P_v = P_k - 2; both MFMA split kernels
-    (key-only pages through the page-pair kernel's FP16 segments or the
-    streaming kernel's) and the generic kernel."""
+    P_v = 0 (every value FP16) and P_v = P_k - 2; the MFMA kernel (key-only
+    pages in its FP16 segments) at GQA 4, 8 and 16, and the generic kernel."""
     from kitty.kernels import paged_attention_batched
     S = 32 if D == 128 else 40
     ctx = [S + 6 * G + 17, S + 3 * G, S + 2 * G + G - 1, S + 1 * G + 5, S + 9 * G + 60]
@@ -306,7 +303,7 @@ def test_independent_value_stream(dev, kernel, Hq, H, D, G, dk):
     out = paged_attention_batched(
         c["q"].to(dev), c["bt"].to(dev), i32(npk), kb, kh, km, vp, vm, c["bi"].to(dev), c["sk"].to(dev),
         c["sv"].to(dev), i32([S] * B), c["tk"].to(dev), tv.to(dev), i32(c["tails"]),
-        num_pages_v=i32(npv), tail_len_v=i32(nv), stream_kernel=kernel == "stream").cpu().numpy()
+        num_pages_v=i32(npv), tail_len_v=i32(nv)).cpu().numpy()
     pools = [t.numpy() for t in c["pools"]]
     for b in range(B):
         bt = c["bt"][b].numpy()

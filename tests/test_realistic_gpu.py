@@ -34,9 +34,6 @@ GQ16 = dict(B=2, Hq=128, Hkv=8, ctx=32768, boost=0.125, outlier=16.0, seed=16)
 
 @pytest.mark.parametrize("name,seqs", [("cfg3", (0, 7, 15)), ("cfg5", (0, 3)), ("gq16", (0, 1))])
 def test_benchmark_workload_parity(dev, name, seqs):
-    """Both MFMA split kernels (page-pair, the default, and streaming) on
-    the benchmark's pools."""
-    from kitty.kernels.ops import DecodePlan
     bench = _bench()
     cfg = GQ16 if name == "gq16" else bench.CONFIGS[name]
     # pages to sample: the first, middle and last pages of two sequences (ids
@@ -72,20 +69,11 @@ def test_benchmark_workload_parity(dev, name, seqs):
             assert np.array_equal(vm[pid, h, :, 1].view(np.uint16), np.asarray(zv).view(np.uint16))
     print(f"realistic {name}: {len(want)} pages x {H} heads bit-exact; decoding", flush=True)
     out = w["plans"][0].run().float().cpu().numpy()
-    B = w["B"]
-    streaming = DecodePlan(w["q"], w["tables"][0], torch.tensor(w["np_list"], dtype=torch.int32, device=dev),
-                           *w["pools"], w["bi"], w["sk"], w["sv"], torch.full((B,), bench.S, dtype=torch.int32,
-                                                                              device=dev),
-                           w["tk"], w["tv"], torch.tensor(w["tail_list"], dtype=torch.int32, device=dev),
-                           out=torch.empty_like(w["out"]), stream_kernel=True)
-    out_s = streaming.run().float().cpu().numpy()
-    assert np.isfinite(out).all() and np.isfinite(out_s).all()
+    assert np.isfinite(out).all()
     q, sk, sv_, tk, tv = (t.cpu().numpy() for t in (w["q"], w["sk"], w["sv"], w["tk"], w["tv"]))
     for b in seqs:
         n, t = w["np_list"][b], w["tail_list"][b]
         ref = O.paged_attention(q[b], bt0[b, :n].numpy(), kb, kh, km, vp, vm, bi, dk, sk[b], sv_[b],
                                 tk[b, :, :t], tv[b, :, :t], w["Hq"], H, D).astype(np.float32)
-        for kern, o in (("page-pair", out), ("streaming", out_s)):
-            err = np.abs(o[b] - ref) - (ATOL + RTOL * np.abs(ref))
-            assert (err <= 0).all(), (f"{name} {kern} b={b}: max excess {err.max():.3g}, "
-                                      f"max |diff| {np.abs(o[b] - ref).max():.3g}")
+        err = np.abs(out[b] - ref) - (ATOL + RTOL * np.abs(ref))
+        assert (err <= 0).all(), f"{name} b={b}: max excess {err.max():.3g}, max |diff| {np.abs(out[b] - ref).max():.3g}"

@@ -35,10 +35,10 @@ def _noalloc(plan):
     return out
 
 
-@pytest.mark.parametrize("kernel", ["page_pair", "stream", "generic"])
+@pytest.mark.parametrize("kernel", ["mfma", "generic"])
 def test_noalloc_matches_workspace_decode(dev, kernel):
     from kitty.kernels.ops import DecodePlan  # noqa: F401  (library loads first)
-    kw = {"stream_kernel": True} if kernel == "stream" else {}
+    kw = {}
     if kernel == "generic":
         shapes = [(5, 8, 4, 64, 32, 8, [40 + 9 * 32 + 3, 40 + 2 * 32, 40, 40 + 17 * 32 + 31, 40 + 5 * 32 + 1]),
                   (2, 8, 4, 64, 32, 8, [40 + 3 * 32 + 7, 40 + 32])]
