@@ -38,7 +38,7 @@ struct DecodeParams {
     // page_waves waves, each at least min_chunk units; fp16_weight = units
     // charged per 128 sink + tail tokens.
     int balanced, page_waves, min_chunk, fp16_weight;
-    int fp16_units;  // FP16 units per pair: seq_fp16_units(sink_cap + tail_cap, fp16_weight)
+    int fp16_units;  // FP16 units per pair: seq_fp16_units(sink_cap + tail_v_cap, fp16_weight)
     float *ws_o;  // uniform: [B][Hq][num_partials][D]; balanced: [partial t][GQ][D]
     float *ws_ml; // the same rows: running max (log2 domain) and sum
     int *ws_pair; // balanced: [B * Hkv][2] first and last partial t of each (b, kh)
@@ -115,18 +115,6 @@ __host__ __device__ inline int seq_page_units(int np_raw, int max_pages, int fp1
 __host__ __device__ inline int seq_fp16_units(int ntok, int weight)
 {
     return ntok > 0 ? (int)(((int64_t)ntok * weight + 127) / 128) : 0;
-}
-// Page units of sequence b (its full pages, npv: key and value both
-// quantised) and whether it is bad.
-struct SeqUnits1 {
-    int npu;
-    bool bad;
-};
-
-__device__ __forceinline__ SeqUnits1 seq_units(const DecodeParams &p, int b)
-{
-    const SeqLens L = seq_lens(p, b);
-    return SeqUnits1{seq_page_units(L.bad ? -1 : L.npv, p.max_pages, p.fp16_units), L.bad};
 }
 
 // working waves for U units: at most page_waves, each at least min_chunk units
