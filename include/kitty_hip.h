@@ -8,7 +8,9 @@
  * types.  Conventions:
  *   - every pointer argument is a device pointer unless stated otherwise;
  *   - strides are in elements of the pointed-to type;
- *   - fp16 data is passed as uint16_t bit patterns;
+ *   - fp16 data is passed as uint16_t bit patterns, and so is bf16 data where
+ *     a *_dtype field selects it (KittyConfig.dtype = "bfloat16",
+ *     kitty/config.py:76, layout.py:123-137, pipeline.py:83-106);
  *   - calls are asynchronous on the given stream, never allocate device
  *     memory and never synchronise;
  *   - the return value is KITTY_OK or a negative KITTY_E_* code, and
@@ -24,7 +26,11 @@
 extern "C" {
 #endif
 
-#define KITTY_ABI_VERSION 2
+#define KITTY_ABI_VERSION 3
+
+/* Element type of 16-bit data (the *_dtype fields below). */
+#define KITTY_DTYPE_F16 0
+#define KITTY_DTYPE_BF16 1
 
 #define KITTY_OK 0
 #define KITTY_E_INVALID (-1)     /* bad shape, stride, alignment or null pointer */
@@ -47,9 +53,13 @@ const char *kitty_last_error(void);
  * elements (bytes for the uint8 pools).
  *   key_low   (P, H, D, G/4) u8      — Tensor_2bits, low 2 bits of every channel
  *   key_high  (P, H, Dk, G/4) u8     — Tensor_High_2bits, high 2 bits of boosted channels
- *   key_scale / key_zero  (P, H, D)  — rows 0 / 1 of key_metadata (P, H, 2, D) fp16
+ *   key_scale / key_zero  (P, H, D)  — rows 0 / 1 of key_metadata (P, H, 2, D) fp16 or bf16
  *   value     (P, H, G, D/4) u8      — value_pool, 4 channels per byte
- *   value_scale / value_zero (P, H, G) — columns 0 / 1 of value_metadata (P, H, G, 2) fp16
+ *   value_scale / value_zero (P, H, G) — columns 0 / 1 of value_metadata (P, H, G, 2) fp16 or bf16
+ * meta_dtype gives the metadata pools' type.  The reference computes every
+ * scale and zero point as fp16 and copies it into the pool's dtype
+ * (quantize_key.py:121-122, 263-269; quantize_value.py:90, 223-227), so a
+ * bf16 pool holds bf16(fp16(x)), both roundings to nearest even.
  */
 typedef struct {
     uint8_t *key_low;
@@ -70,6 +80,7 @@ typedef struct {
     int32_t head_dim;     /* D, multiple of 4 */
     int32_t page_tokens;  /* G, multiple of 4 */
     int32_t d_boost;      /* Dk = KittyConfig.d_boost */
+    int32_t meta_dtype;   /* KITTY_DTYPE_F16 or KITTY_DTYPE_BF16 (ABI version 3) */
 } kitty_page_store;
 
 /* ------------------------------------------------- batch quantize + pack
@@ -79,7 +90,8 @@ typedef struct {
  * (kitty/kernels/quantize_value.py:197-227) once per (layer, head), with one
  * launch for all blocks of a spill.
  *
- * Block (o, i), o < n_outer, i < n_inner, quantises the G x D fp16 block
+ * Block (o, i), o < n_outer, i < n_inner, quantises the G x D fp16 (or, with
+ * src_dtype KITTY_DTYPE_BF16, bf16) block
  *   key[o*key_s_outer + i*key_s_inner + t*key_s_tok + d*key_s_chan]
  * per channel (INT4 when boost_idx[d] < sentinel, else INT2) and the value
  * block (same indexing with value_*) per token, and writes them to
@@ -101,28 +113,35 @@ typedef struct {
     int32_t n_outer, n_inner;
     int32_t value_rows;
     int32_t sentinel; /* KittyConfig.sentinel = min(d_boost + 1, 255) */
+    int32_t src_dtype; /* key / value blocks: KITTY_DTYPE_F16 or KITTY_DTYPE_BF16 (ABI version 3) */
 } kitty_quant_batch;
 
 int kitty_quantize_kv_blocks(const kitty_page_store *store, const kitty_quant_batch *batch,
                              kitty_stream_t stream);
 
+/* Output type of the page dequantisers: the launchers write into a caller
+ * tensor of any of these (dequantize_key.py:228 converts to out.dtype). */
+#define KITTY_OUT_F16 0
+#define KITTY_OUT_F32 1
+#define KITTY_OUT_BF16 2
+
 /* ------------------------------------------------ key page dequantize
  * Replaces dequantize_key_page (kitty/kernels/dequantize_key.py:169-228) and
  * dequantize_key_page_torch (:35-97):
  * out[d*out_s_chan + t] = ((low | high<<2) - zero[d]) * scale[d], computed in
- * fp32 and stored as fp32 (out_fp32 != 0, the _torch variant's result) or
- * fp16, reading page `page`, head `head` of `store` and boost row
- * `boost_idx` (D,). */
+ * fp32 and stored as out_kind (KITTY_OUT_F32: the _torch variant's result;
+ * KITTY_OUT_F16 / KITTY_OUT_BF16: rounded to nearest even), reading page
+ * `page`, head `head` of `store` and boost row `boost_idx` (D,). */
 int kitty_dequantize_key_page(const kitty_page_store *store, int64_t page, int32_t head,
-                              const uint8_t *boost_idx, void *out, int64_t out_s_chan, int32_t out_fp32,
+                              const uint8_t *boost_idx, void *out, int64_t out_s_chan, int32_t out_kind,
                               kitty_stream_t stream);
 
 /* ---------------------------------------------- value page dequantize
  * Replaces dequantize_value_page_torch (kitty/kernels/quantize_value.py:97-133):
- * out[t*out_s_tok + d] = (code - zero[t]) * scale[t] in fp32, stored as fp32
- * (out_fp32 != 0) or fp16, for page `page`, head `head` of `store`. */
+ * out[t*out_s_tok + d] = (code - zero[t]) * scale[t] in fp32, stored as
+ * out_kind (KITTY_OUT_*), for page `page`, head `head` of `store`. */
 int kitty_dequantize_value_page(const kitty_page_store *store, int64_t page, int32_t head, void *out,
-                                int64_t out_s_tok, int32_t out_fp32, kitty_stream_t stream);
+                                int64_t out_s_tok, int32_t out_kind, kitty_stream_t stream);
 
 /* ------------------------------------------- paged decode attention
  * Replaces paged_attention / paged_attention_reference
@@ -206,10 +225,28 @@ typedef struct {
     const int32_t *num_pages_v; /* (B,) value pages per sequence */
     const int32_t *tail_len_v;  /* (B,) value-tail tokens per sequence, read from tail_v */
     int32_t tail_v_capacity;    /* tokens allocated per (seq, head) in tail_v (tail_len_v set) */
+
+    /* element types (ABI version 3): the metadata pools, and q with the
+     * sinks and tails.  out is fp16 either way, as the reference returns
+     * (kitty/kernels/attention.py:189).  bf16 runs the shape-generic kernel. */
+    int32_t meta_dtype; /* KITTY_DTYPE_F16 or KITTY_DTYPE_BF16 */
+    int32_t act_dtype;  /* KITTY_DTYPE_F16 or KITTY_DTYPE_BF16 */
 } kitty_decode_args;
 
 int kitty_decode_workspace_size(const kitty_decode_args *args, size_t *bytes);
 int kitty_paged_decode(const kitty_decode_args *args, kitty_stream_t stream);
+
+/* Which split kernel kitty_paged_decode runs for these arguments:
+ * *path = KITTY_DECODE_PATH_MFMA (the production kernel: D = G = 128,
+ * Dk <= 32, GQA 4 / 8 / 16, fp16, 16-byte aligned buffers, unique boost
+ * ranks) or KITTY_DECODE_PATH_GENERIC (every other shape the reference
+ * accepts, about 15x slower at the production shape).  Mirrors the
+ * dispatch decision of paged_attention (kitty/kernels/attention.py:320-341),
+ * so callers can see when a profile with repeated ranks or a misaligned
+ * buffer sends decode to the slower kernel. */
+#define KITTY_DECODE_PATH_GENERIC 0
+#define KITTY_DECODE_PATH_MFMA 1
+int kitty_decode_path(const kitty_decode_args *args, int32_t *path);
 
 /* The two phases of kitty_paged_decode, for callers that interleave other
  * work or time the phases: _splits writes the split-K partials to the
@@ -272,11 +309,12 @@ int kitty_append_tokens(const kitty_append_args *args, kitty_stream_t stream);
 /* ------------------------------------------- sensitivity accumulation
  * Replaces _ChannelAccumulator.update (kitty/sensitivity.py:46-61):
  * out[h*head_dim + d] += sum over b < batch, t < tokens of
- * |key[b*s_b + t*s_t + h*s_h + d]| in fp32, key fp16 with a contiguous
- * channel dimension (the hook's (B, H, T, D) view of a key projection).
- * The summation order is fixed, so repeated runs give identical sums. */
+ * |key[b*s_b + t*s_t + h*s_h + d]| in fp32, key fp16 or bf16 (key_dtype,
+ * the model's dtype) with a contiguous channel dimension (the hook's
+ * (B, H, T, D) view of a key projection).  The summation order is fixed, so
+ * repeated runs give identical sums. */
 int kitty_channel_abs_sum(const uint16_t *key, int64_t s_b, int64_t s_t, int64_t s_h, int32_t batch,
-                          int32_t tokens, int32_t num_kv_heads, int32_t head_dim, float *out,
+                          int32_t tokens, int32_t num_kv_heads, int32_t head_dim, int32_t key_dtype, float *out,
                           kitty_stream_t stream);
 
 #ifdef __cplusplus

@@ -112,6 +112,9 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
         return fail(KITTY_E_INVALID, "num_pages_v and tail_len_v go together (both NULL: one stream length)");
     if (a.tail_len_v && a.tail_v_capacity < 0)
         return fail(KITTY_E_INVALID, "tail_v_capacity must be >= 0");
+    if ((a.meta_dtype != KITTY_DTYPE_F16 && a.meta_dtype != KITTY_DTYPE_BF16) ||
+        (a.act_dtype != KITTY_DTYPE_F16 && a.act_dtype != KITTY_DTYPE_BF16))
+        return fail(KITTY_E_INVALID, "meta_dtype and act_dtype must be KITTY_DTYPE_F16 or KITTY_DTYPE_BF16");
     p = DecodeParams{};
     p.q = a.q;
     p.q_s_seq = a.q_s_seq;
@@ -149,6 +152,8 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
     p.Dk = a.d_boost;
     p.max_pages = a.max_pages;
     p.flags = a.flags;
+    p.meta_bf16 = a.meta_dtype == KITTY_DTYPE_BF16;
+    p.act_bf16 = a.act_dtype == KITTY_DTYPE_BF16;
     p.sm_scale = a.sm_scale;
     set_plan(p, a, mfma_path_supported(p));
     return KITTY_OK;
@@ -196,6 +201,18 @@ extern "C" int kitty_decode_workspace_size(const kitty_decode_args *args, size_t
         n = std::max(n, workspace_bytes(o));
     }
     *bytes = n;
+    return KITTY_OK;
+}
+
+extern "C" int kitty_decode_path(const kitty_decode_args *args, int32_t *path)
+{
+    DecodeParams p;
+    int rc = build_params(args, p);
+    if (rc)
+        return rc;
+    if (!path)
+        return fail(KITTY_E_INVALID, "path is NULL");
+    *path = mfma_path_supported(p) ? KITTY_DECODE_PATH_MFMA : KITTY_DECODE_PATH_GENERIC;
     return KITTY_OK;
 }
 

@@ -33,6 +33,8 @@ struct DecodeParams {
     int max_pages, pages_per_split, n_splits;
     int n_fp16;   // FP16 splits per (b, kh) of the uniform plan (one)
     int flags;
+    int meta_bf16; // metadata pools hold bf16 (else fp16)
+    int act_bf16;  // q, sinks and tails hold bf16 (else fp16)
     float sm_scale;
     // Unit-balanced plan of the MFMA kernel (balanced = 1): the grid has
     // page_waves waves, each at least min_chunk units; fp16_weight = units

@@ -178,9 +178,10 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
     s.vzero = (float *)carve(sizeof(float) * G);
 
     const float qscale = p.sm_scale * kLog2e;
+    const bool mbf = p.meta_bf16 != 0, abf = p.act_bf16 != 0;  // bf16 metadata / activations
     for (int e = tid; e < GQ * D; e += kGenThreads) {
         const int g = e / D, d = e - g * D;
-        s.qs[e] = h2f(p.q[b * p.q_s_seq + (int64_t)(kh * GQ + g) * p.q_s_head + d]) * qscale;
+        s.qs[e] = x2f(p.q[b * p.q_s_seq + (int64_t)(kh * GQ + g) * p.q_s_head + d], abf) * qscale;
         s.O[e] = 0.0f;
     }
     if (tid < GQ) {
@@ -199,8 +200,8 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
         if (Dk > 0)
             copy_bytes(s.khigh, p.key_high + ph * Dk * G4, Dk * G4);
         for (int e = tid; e < D; e += kGenThreads) {
-            s.kscale[e] = h2f(p.key_meta[ph * 2 * D + e]);
-            s.kzero[e] = h2f(p.key_meta[ph * 2 * D + D + e]);
+            s.kscale[e] = x2f(p.key_meta[ph * 2 * D + e], mbf);
+            s.kzero[e] = x2f(p.key_meta[ph * 2 * D + D + e], mbf);
         }
     };
     // k = ((low | high << 2) - z) * s  (dequantize_key.py:73-95)
@@ -225,8 +226,8 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
             stage_key_page(ph);
             copy_bytes(s.vcode, p.value + ph * G * D4, G * D4);
             for (int e = tid; e < G; e += kGenThreads) {
-                s.vscale[e] = h2f(p.value_meta[ph * 2 * G + 2 * e]);
-                s.vzero[e] = h2f(p.value_meta[ph * 2 * G + 2 * e + 1]);
+                s.vscale[e] = x2f(p.value_meta[ph * 2 * G + 2 * e], mbf);
+                s.vzero[e] = x2f(p.value_meta[ph * 2 * G + 2 * e + 1], mbf);
             }
             __syncthreads();
             // v = (code - z_t) * s_t  (quantize_value.py:118-133)
@@ -245,8 +246,8 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
         const uint16_t *tvb = p.tail_v.ptr + b * p.tail_v.s_seq + kh * p.tail_v.s_head;
         for (int t0 = 0; t0 < L.ns; t0 += kChunkMax) {
             const int c = min(kChunkMax, L.ns - t0);
-            auto kval = [&](int d, int t) -> float { return h2f(skb[(int64_t)(t0 + t) * p.sink_k.s_tok + d]); };
-            auto vval = [&](int t, int d) -> float { return h2f(svb[(int64_t)(t0 + t) * p.sink_v.s_tok + d]); };
+            auto kval = [&](int d, int t) -> float { return x2f(skb[(int64_t)(t0 + t) * p.sink_k.s_tok + d], abf); };
+            auto vval = [&](int t, int d) -> float { return x2f(svb[(int64_t)(t0 + t) * p.sink_v.s_tok + d], abf); };
             gen_chunk<GQ>(s, D, c, kval, vval);
         }
         for (int pi = L.npv; pi < L.npk && !poison; ++pi) {
@@ -258,14 +259,14 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
             stage_key_page((int64_t)page * H + kh);
             __syncthreads();
             const int64_t r0 = (int64_t)(pi - L.npv) * G;  // the page's rows of the value tail
-            auto vval = [&](int t, int d) -> float { return h2f(tvb[(r0 + t) * p.tail_v.s_tok + d]); };
+            auto vval = [&](int t, int d) -> float { return x2f(tvb[(r0 + t) * p.tail_v.s_tok + d], abf); };
             gen_chunk<GQ>(s, D, G, kpage, vval);
         }
         for (int t0 = 0; t0 < L.nk && !poison; t0 += kChunkMax) {
             const int c = min(kChunkMax, L.nk - t0);
-            auto kval = [&](int d, int t) -> float { return h2f(tkb[(int64_t)(t0 + t) * p.tail_k.s_tok + d]); };
+            auto kval = [&](int d, int t) -> float { return x2f(tkb[(int64_t)(t0 + t) * p.tail_k.s_tok + d], abf); };
             auto vval = [&](int t, int d) -> float {
-                return h2f(tvb[(int64_t)(L.nmix + t0 + t) * p.tail_v.s_tok + d]);
+                return x2f(tvb[(int64_t)(L.nmix + t0 + t) * p.tail_v.s_tok + d], abf);
             };
             gen_chunk<GQ>(s, D, c, kval, vval);
         }

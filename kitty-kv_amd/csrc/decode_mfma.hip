@@ -1357,7 +1357,8 @@ static bool seg_aligned(const kitty_fp16_seg &s)
 
 bool mfma_shape_supported(const DecodeParams &p)
 {
-    return p.D == 128 && p.G == 128 && p.Dk >= 0 && p.Dk <= 32 && (p.GQ == 4 || p.GQ == 8 || p.GQ == 16);
+    return p.D == 128 && p.G == 128 && p.Dk >= 0 && p.Dk <= 32 && (p.GQ == 4 || p.GQ == 8 || p.GQ == 16) &&
+           !p.meta_bf16 && !p.act_bf16;
 }
 
 bool mfma_path_supported(const DecodeParams &p)

@@ -22,8 +22,9 @@ __device__ void quantize_key_block(const QuantLaunch &L, int o, int i, unsigned 
     const kitty_quant_batch &qb = L.qb;
     const int D = st.head_dim, G = st.page_tokens, G4 = G / 4, Dk = st.d_boost;
     const int tid = threadIdx.x;
+    const bool sbf = qb.src_dtype == KITTY_DTYPE_BF16, mbf = st.meta_dtype == KITTY_DTYPE_BF16;
 
-    uint16_t *tile = (uint16_t *)smem;                      // G*D
+    uint16_t *tile = (uint16_t *)smem;                      // G*D (fp16 or bf16 bits)
     uint8_t *brow = (uint8_t *)(tile + G * D);              // D
     uint8_t *hbytes = brow + ((D + 15) & ~15);              // D*G4
     float *red_mn = (float *)(hbytes + ((D * G4 + 15) & ~15)); // 256
@@ -52,7 +53,7 @@ __device__ void quantize_key_block(const QuantLaunch &L, int o, int i, unsigned 
 
     float mn = __builtin_inff(), mx = -__builtin_inff();
     for (int t = 4 * j0; t < 4 * j1; ++t) {
-        float v = h2f(tile[t * D + d]);
+        float v = x2f(tile[t * D + d], sbf);
         mn = v < mn ? v : mn;
         mx = v > mx ? v : mx;
     }
@@ -78,7 +79,7 @@ __device__ void quantize_key_block(const QuantLaunch &L, int o, int i, unsigned 
             uint32_t lo = 0, hi = 0;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                uint32_t c = quant_code(h2f(tile[(4 * j + k) * D + d]), s, z, mq);
+                uint32_t c = quant_code(x2f(tile[(4 * j + k) * D + d], sbf), s, z, mq);
                 lo |= (c & 3u) << (2 * k);
                 hi |= ((c >> 2) & 3u) << (2 * k);
             }
@@ -86,8 +87,8 @@ __device__ void quantize_key_block(const QuantLaunch &L, int o, int i, unsigned 
             hbytes[d * G4 + j] = (uint8_t)hi;
         }
         if (sl == 0) {                                             // :121-122
-            st.key_scale[page * st.key_meta_s_page + i * st.key_meta_s_head + d * st.key_meta_s_chan] = f2h(s);
-            st.key_zero[page * st.key_meta_s_page + i * st.key_meta_s_head + d * st.key_meta_s_chan] = f2h(z);
+            st.key_scale[page * st.key_meta_s_page + i * st.key_meta_s_head + d * st.key_meta_s_chan] = meta_store(s, mbf);
+            st.key_zero[page * st.key_meta_s_page + i * st.key_meta_s_head + d * st.key_meta_s_chan] = meta_store(z, mbf);
         }
     }
     __syncthreads();
@@ -114,6 +115,7 @@ __device__ void quantize_value_block(const QuantLaunch &L, int o, int i, unsigne
     const kitty_quant_batch &qb = L.qb;
     const int D = st.head_dim, G = st.page_tokens, D4 = D / 4;
     const int tid = threadIdx.x;
+    const bool sbf = qb.src_dtype == KITTY_DTYPE_BF16, mbf = st.meta_dtype == KITTY_DTYPE_BF16;
     float *red_mn = (float *)smem;
     float *red_mx = red_mn + kQuantThreads;
 
@@ -128,7 +130,7 @@ __device__ void quantize_value_block(const QuantLaunch &L, int o, int i, unsigne
     const bool real = t < qb.value_rows; // rows past value_rows are the zero padding
 
     auto load = [&](int d) -> float {
-        return real ? h2f(src[(int64_t)t * qb.value_s_tok + (int64_t)d * qb.value_s_chan]) : 0.0f;
+        return real ? x2f(src[(int64_t)t * qb.value_s_tok + (int64_t)d * qb.value_s_chan], sbf) : 0.0f;
     };
     float mn = __builtin_inff(), mx = -__builtin_inff();
     for (int d = 4 * j0; d < 4 * j1; ++d) {
@@ -161,8 +163,8 @@ __device__ void quantize_value_block(const QuantLaunch &L, int o, int i, unsigne
     }
     if (sl == 0) {                                                 // :90
         const int64_t m = page * st.value_meta_s_page + i * st.value_meta_s_head + t * st.value_meta_s_tok;
-        st.value_scale[m] = f2h(s);
-        st.value_zero[m] = f2h(z);
+        st.value_scale[m] = meta_store(s, mbf);
+        st.value_zero[m] = meta_store(z, mbf);
     }
 }
 
@@ -184,19 +186,21 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_kv_kernel(QuantLaunch 
 }
 
 // -------------------------------------------------- key page dequantize
-// out[d][t] = ((low | high << 2) - z[d]) * s[d] (dequantize_key.py:66-97) as fp16.
-__device__ __forceinline__ void store_out(void *out, int64_t idx, int fp32, float v)
+// out[d][t] = ((low | high << 2) - z[d]) * s[d] (dequantize_key.py:66-97),
+// stored as out_kind (KITTY_OUT_*).
+__device__ __forceinline__ void store_out(void *out, int64_t idx, int kind, float v)
 {
-    if (fp32)
+    if (kind == KITTY_OUT_F32)
         ((float *)out)[idx] = v;
     else
-        ((uint16_t *)out)[idx] = f2h(v);
+        ((uint16_t *)out)[idx] = f2x(v, kind == KITTY_OUT_BF16);
 }
 
 __global__ __launch_bounds__(256) void dequantize_key_kernel(kitty_page_store st, int64_t page, int32_t head,
                                                              const uint8_t *boost, void *out, int64_t out_s,
-                                                             int fp32)
+                                                             int kind)
 {
+    const bool mbf = st.meta_dtype == KITTY_DTYPE_BF16;
     const int D = st.head_dim, G = st.page_tokens;
     for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < D * G; e += gridDim.x * blockDim.x) {
         const int d = e / G, t = e - d * G;
@@ -209,22 +213,23 @@ __global__ __launch_bounds__(256) void dequantize_key_kernel(kitty_page_store st
             code |= ((hi[j] >> (2 * k)) & 3) << 2;
         }
         const int64_t m = page * st.key_meta_s_page + head * st.key_meta_s_head + d * st.key_meta_s_chan;
-        const float s = h2f(st.key_scale[m]), z = h2f(st.key_zero[m]);
-        store_out(out, d * out_s + t, fp32, ((float)code - z) * s);
+        const float s = x2f(st.key_scale[m], mbf), z = x2f(st.key_zero[m], mbf);
+        store_out(out, d * out_s + t, kind, ((float)code - z) * s);
     }
 }
 
-// out[t][d] = (code - z[t]) * s[t] (quantize_value.py:118-133) as fp16.
+// out[t][d] = (code - z[t]) * s[t] (quantize_value.py:118-133), stored as out_kind.
 __global__ __launch_bounds__(256) void dequantize_value_kernel(kitty_page_store st, int64_t page, int32_t head,
-                                                               void *out, int64_t out_s, int fp32)
+                                                               void *out, int64_t out_s, int kind)
 {
+    const bool mbf = st.meta_dtype == KITTY_DTYPE_BF16;
     const int D = st.head_dim, G = st.page_tokens;
     for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < D * G; e += gridDim.x * blockDim.x) {
         const int t = e / D, d = e - t * D;
         const uint8_t *row = st.value + page * st.value_s_page + head * st.value_s_head + t * st.value_s_row;
         const int code = (row[d >> 2] >> (2 * (d & 3))) & 3;
         const int64_t m = page * st.value_meta_s_page + head * st.value_meta_s_head + t * st.value_meta_s_tok;
-        store_out(out, t * out_s + d, fp32, ((float)code - h2f(st.value_zero[m])) * h2f(st.value_scale[m]));
+        store_out(out, t * out_s + d, kind, ((float)code - x2f(st.value_zero[m], mbf)) * x2f(st.value_scale[m], mbf));
     }
 }
 
@@ -238,6 +243,8 @@ static int validate_store(const kitty_page_store *st)
         return fail(KITTY_E_UNSUPPORTED, "head_dim, page_tokens <= 256 and head_dim*page_tokens <= 32768 are supported");
     if (st->d_boost < 0 || st->d_boost > st->head_dim)
         return fail(KITTY_E_INVALID, "d_boost must be in [0, head_dim]");
+    if (st->meta_dtype != KITTY_DTYPE_F16 && st->meta_dtype != KITTY_DTYPE_BF16)
+        return fail(KITTY_E_INVALID, "meta_dtype must be KITTY_DTYPE_F16 or KITTY_DTYPE_BF16");
     return KITTY_OK;
 }
 
@@ -267,6 +274,8 @@ extern "C" int kitty_quantize_kv_blocks(const kitty_page_store *store, const kit
         return fail(KITTY_E_INVALID, "value quantisation needs value pools");
     if (qb.value_rows < 0 || qb.value_rows > store->page_tokens)
         return fail(KITTY_E_INVALID, "value_rows must be in [0, page_tokens]");
+    if (qb.src_dtype != KITTY_DTYPE_F16 && qb.src_dtype != KITTY_DTYPE_BF16)
+        return fail(KITTY_E_INVALID, "src_dtype must be KITTY_DTYPE_F16 or KITTY_DTYPE_BF16");
     const int D = store->head_dim, G = store->page_tokens;
     const size_t key_lds = (size_t)G * D * 2 + ((D + 15) & ~15) + (((size_t)D * (G / 4) + 15) & ~15) +
                            2 * kQuantThreads * sizeof(float);
@@ -287,34 +296,38 @@ extern "C" int kitty_quantize_kv_blocks(const kitty_page_store *store, const kit
 }
 
 extern "C" int kitty_dequantize_key_page(const kitty_page_store *store, int64_t page, int32_t head,
-                                         const uint8_t *boost_idx, void *out, int64_t out_s_chan, int32_t out_fp32,
+                                         const uint8_t *boost_idx, void *out, int64_t out_s_chan, int32_t out_kind,
                                          kitty_stream_t stream)
 {
     int rc = validate_store(store);
     if (rc)
         return rc;
+    if (out_kind != KITTY_OUT_F16 && out_kind != KITTY_OUT_F32 && out_kind != KITTY_OUT_BF16)
+        return fail(KITTY_E_INVALID, "out_kind must be KITTY_OUT_F16, KITTY_OUT_F32 or KITTY_OUT_BF16");
     if (!boost_idx || !out || !store->key_low || !store->key_scale || !store->key_zero)
         return fail(KITTY_E_INVALID, "NULL pointer");
     if (page < 0 || page >= store->num_pages || head < 0 || head >= store->num_kv_heads)
         return fail(KITTY_E_INVALID, "page/head out of range");
     const int n = store->head_dim * store->page_tokens;
     hipLaunchKernelGGL(dequantize_key_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, *store,
-                       page, head, boost_idx, out, out_s_chan, (int)(out_fp32 != 0));
+                       page, head, boost_idx, out, out_s_chan, (int)out_kind);
     return check_launch("dequantize_key_kernel");
 }
 
 extern "C" int kitty_dequantize_value_page(const kitty_page_store *store, int64_t page, int32_t head,
-                                           void *out, int64_t out_s_tok, int32_t out_fp32, kitty_stream_t stream)
+                                           void *out, int64_t out_s_tok, int32_t out_kind, kitty_stream_t stream)
 {
     int rc = validate_store(store);
     if (rc)
         return rc;
+    if (out_kind != KITTY_OUT_F16 && out_kind != KITTY_OUT_F32 && out_kind != KITTY_OUT_BF16)
+        return fail(KITTY_E_INVALID, "out_kind must be KITTY_OUT_F16, KITTY_OUT_F32 or KITTY_OUT_BF16");
     if (!out || !store->value || !store->value_scale || !store->value_zero)
         return fail(KITTY_E_INVALID, "NULL pointer");
     if (page < 0 || page >= store->num_pages || head < 0 || head >= store->num_kv_heads)
         return fail(KITTY_E_INVALID, "page/head out of range");
     const int n = store->head_dim * store->page_tokens;
     hipLaunchKernelGGL(dequantize_value_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, *store,
-                       page, head, out, out_s_tok, (int)(out_fp32 != 0));
+                       page, head, out, out_s_tok, (int)out_kind);
     return check_launch("dequantize_value_kernel");
 }

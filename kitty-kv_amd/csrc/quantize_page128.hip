@@ -362,6 +362,8 @@ bool page128_supported(const kitty_page_store &st, const kitty_quant_batch &qb)
 {
     if (st.head_dim != 128 || st.page_tokens != 128)
         return false;
+    if (st.meta_dtype != KITTY_DTYPE_F16 || qb.src_dtype != KITTY_DTYPE_F16)
+        return false;  // bf16 blocks or pools: the shape-generic kernel
     if (qb.key) {
         if (qb.key_s_chan != 1 || !al16(qb.key) || !mul(qb.key_s_outer, 8) || !mul(qb.key_s_inner, 8) ||
             !mul(qb.key_s_tok, 8))

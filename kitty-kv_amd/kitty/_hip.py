@@ -18,7 +18,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 # KITTY_HIP_LIBRARY selects another build of the same ABI (e.g. a tuning variant).
 LIB_PATH = os.environ.get("KITTY_HIP_LIBRARY") or os.path.join(_HERE, "libkitty_hip.so")
 
-KITTY_ABI_VERSION = 2
+KITTY_ABI_VERSION = 3
 KITTY_OK = 0
 KITTY_E_INVALID = -1
 KITTY_E_HIP = -2
@@ -26,6 +26,20 @@ KITTY_E_UNSUPPORTED = -3
 KITTY_E_EXHAUSTED = -4
 KITTY_E_NOT_FOUND = -5
 KITTY_DECODE_UNIQUE_BOOST_ROWS = 1
+KITTY_DTYPE_F16 = 0
+KITTY_DTYPE_BF16 = 1
+KITTY_OUT_F16, KITTY_OUT_F32, KITTY_OUT_BF16 = 0, 1, 2
+KITTY_DECODE_PATH_GENERIC, KITTY_DECODE_PATH_MFMA = 0, 1
+
+
+def dtype_code(t: torch.Tensor, name: str) -> int:
+    """KITTY_DTYPE_* of a 16-bit float tensor (fp16 or bf16, the two dtypes
+    KittyConfig allows, config.py:76)."""
+    if t.dtype == torch.float16:
+        return KITTY_DTYPE_F16
+    if t.dtype == torch.bfloat16:
+        return KITTY_DTYPE_BF16
+    raise ValueError(f"{name} must be float16 or bfloat16, got {t.dtype}")
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -44,6 +58,7 @@ class PageStore(ctypes.Structure):
         ("value_meta_s_page", _i64), ("value_meta_s_head", _i64), ("value_meta_s_tok", _i64),
         ("num_pages", _i64),
         ("num_kv_heads", _i32), ("head_dim", _i32), ("page_tokens", _i32), ("d_boost", _i32),
+        ("meta_dtype", _i32),
     ]
 
 
@@ -55,6 +70,7 @@ class QuantBatch(ctypes.Structure):
         ("value_s_chan", _i64),
         ("boost_idx", _vp), ("boost_s_outer", _i64), ("boost_s_inner", _i64),
         ("page_ids", _vp), ("n_outer", _i32), ("n_inner", _i32), ("value_rows", _i32), ("sentinel", _i32),
+        ("src_dtype", _i32),
     ]
 
 
@@ -77,6 +93,7 @@ class DecodeArgs(ctypes.Structure):
         ("flags", _i32), ("sm_scale", ctypes.c_float),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("num_pages_v", _vp), ("tail_len_v", _vp), ("tail_v_capacity", _i32),
+        ("meta_dtype", _i32), ("act_dtype", _i32),
     ]
 
 
@@ -102,7 +119,7 @@ class AppendArgs(ctypes.Structure):
 EXPORTED_SYMBOLS = (
     "kitty_abi_version", "kitty_last_error", "kitty_quantize_kv_blocks",
     "kitty_dequantize_key_page", "kitty_dequantize_value_page",
-    "kitty_decode_workspace_size", "kitty_paged_decode", "kitty_paged_decode_splits",
+    "kitty_decode_workspace_size", "kitty_decode_path", "kitty_paged_decode", "kitty_paged_decode_splits",
     "kitty_paged_decode_merge", "kitty_paged_decode_noalloc", "kitty_append_tokens", "kitty_channel_abs_sum",
 )
 
@@ -129,12 +146,13 @@ def load() -> ctypes.CDLL:
     L.kitty_dequantize_key_page.argtypes = [ctypes.POINTER(PageStore), _i64, _i32, _vp, _vp, _i64, _i32, _vp]
     L.kitty_dequantize_value_page.argtypes = [ctypes.POINTER(PageStore), _i64, _i32, _vp, _i64, _i32, _vp]
     L.kitty_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t)]
+    L.kitty_decode_path.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_int32)]
     L.kitty_paged_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_paged_decode_splits.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_paged_decode_merge.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_paged_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_append_tokens.argtypes = [ctypes.POINTER(AppendArgs), _vp]
-    L.kitty_channel_abs_sum.argtypes = [_vp, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _vp]
+    L.kitty_channel_abs_sum.argtypes = [_vp, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp]
     if L.kitty_abi_version() != KITTY_ABI_VERSION:
         raise ImportError(f"libkitty_hip ABI {L.kitty_abi_version()} != {KITTY_ABI_VERSION}")
     _lib = L

@@ -91,7 +91,7 @@ class KittyPagedAttention(nn.Module):
 
     def _decode_step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_ids: List[int]) -> torch.Tensor:
         self.pipeline.push_tokens(self.layer_id, k[:, :, 0], v[:, :, 0], seq_ids)
-        qd = q[:, :, 0].to(torch.float16).contiguous()
+        qd = q[:, :, 0].to(self.pipeline.buffer_dtype).contiguous()
         plan = self._plan(qd, seq_ids)
         out = torch.empty(qd.shape, dtype=torch.float16, device=qd.device)
         return plan.run_with(qd, out).unsqueeze(2).to(q.dtype)

@@ -16,17 +16,21 @@ from .quantize_key import _key_store
 def dequantize_key_page(tensor_2bits: torch.Tensor, tensor_high_2bits: torch.Tensor, scale: torch.Tensor,
                         zero_point: torch.Tensor, boost_idx: torch.Tensor, D_boost: int,
                         out: torch.Tensor) -> None:
-    """Dequantise one key page into ``out`` (D, G), fp16 or fp32 (dequantize_key.py:169-228)."""
+    """Dequantise one key page into ``out`` (D, G) of float16, bfloat16 or
+    float32 (dequantize_key.py:169-228: the fp32 result converted to out's
+    dtype)."""
     dev = _hip.require_device(tensor_2bits, tensor_high_2bits, scale, zero_point, boost_idx, out)
     D, G4 = tensor_2bits.shape
-    _need(out.shape == (D, G4 * 4) and out.stride(1) == 1 and out.dtype in (torch.float16, torch.float32),
-          "out must be (D, G) float16/float32 with contiguous rows")
+    kinds = {torch.float16: _hip.KITTY_OUT_F16, torch.float32: _hip.KITTY_OUT_F32,
+             torch.bfloat16: _hip.KITTY_OUT_BF16}
+    _need(out.shape == (D, G4 * 4) and out.stride(1) == 1 and out.dtype in kinds,
+          "out must be (D, G) float16/bfloat16/float32 with contiguous rows")
     _need(boost_idx.dtype == torch.uint8 and boost_idx.shape == (D,) and boost_idx.is_contiguous(),
           "boost_idx must be contiguous uint8 (D,)")
     store = _key_store(D, G4 * 4, D_boost, tensor_2bits, tensor_high_2bits, scale, zero_point)
     _hip.check(_hip.load().kitty_dequantize_key_page(
         ctypes.byref(store), 0, 0, boost_idx.data_ptr(), out.data_ptr(), out.stride(0),
-        1 if out.dtype == torch.float32 else 0, _hip.stream_ptr(dev)))
+        kinds[out.dtype], _hip.stream_ptr(dev)))
 
 
 def dequantize_key_page_torch(tensor_2bits: torch.Tensor, tensor_high_2bits: torch.Tensor, scale: torch.Tensor,

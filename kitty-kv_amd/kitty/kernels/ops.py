@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import warnings
 from typing import Optional, Sequence, Tuple
 
 import torch
@@ -20,10 +21,12 @@ def _need(cond: bool, msg: str) -> None:
         raise ValueError(msg)
 
 
-def _check_fp16(name: str, t: torch.Tensor) -> None:
-    if t.dtype == torch.bfloat16:
-        raise NotImplementedError(f"{name}: bfloat16 buffers are not supported by the HIP kernels (fp16 only)")
-    _need(t.dtype == torch.float16, f"{name} must be float16, got {t.dtype}")
+def _dtype16(name: str, *tensors: torch.Tensor) -> int:
+    """KITTY_DTYPE_* shared by tensors that must all be float16 or all
+    bfloat16 (KittyConfig.dtype, config.py:76)."""
+    codes = {_hip.dtype_code(t, name) for t in tensors if t is not None}
+    _need(len(codes) == 1, f"{name} must all be float16 or all bfloat16")
+    return codes.pop()
 
 
 def _dev_i32(values: Sequence[int], device: torch.device) -> torch.Tensor:
@@ -40,8 +43,7 @@ def pool_store(key_baseline: torch.Tensor, key_boost: torch.Tensor, key_meta: to
     Dk = key_boost.shape[2]
     _need(key_baseline.dtype == torch.uint8 and key_boost.dtype == torch.uint8 and value_pool.dtype == torch.uint8,
           "packed pools must be uint8")
-    _check_fp16("key_metadata", key_meta)
-    _check_fp16("value_metadata", value_meta)
+    meta_dtype = _dtype16("key_metadata and value_metadata", key_meta, value_meta)
     _need(tuple(key_boost.shape[:2]) == (P, H) and key_boost.shape[3] == G4, "key_boost shape")
     _need(tuple(key_meta.shape) == (P, H, 2, D), "key_metadata shape")
     _need(tuple(value_pool.shape) == (P, H, G, D // 4), "value_pool shape")
@@ -64,6 +66,7 @@ def pool_store(key_baseline: torch.Tensor, key_boost: torch.Tensor, key_meta: to
     s.value_meta_s_page, s.value_meta_s_head, s.value_meta_s_tok = value_meta.stride()[:3]
     s.num_pages = P
     s.num_kv_heads, s.head_dim, s.page_tokens, s.d_boost = H, D, G, Dk
+    s.meta_dtype = meta_dtype
     return s
 
 
@@ -78,13 +81,12 @@ def _quant_batch(store: _hip.PageStore, key: Optional[torch.Tensor], value: Opti
           "block shape does not match the pools")
     _need(page_ids.dtype == torch.int32 and page_ids.numel() == n_outer, "page_ids must be int32 (n_outer,)")
     b = _hip.QuantBatch()
+    b.src_dtype = _dtype16("key and value blocks", key, value)
     if key is not None:
-        _check_fp16("key", key)
         _need(tuple(key.shape) == (n_outer, n_inner, G, D), "key shape")
         b.key = key.data_ptr()
         b.key_s_outer, b.key_s_inner, b.key_s_tok, b.key_s_chan = key.stride()
     if value is not None:
-        _check_fp16("value", value)
         _need(tuple(value.shape) == (n_outer, n_inner, G, D), "value shape")
         b.value = value.data_ptr()
         b.value_s_outer, b.value_s_inner, b.value_s_tok, b.value_s_chan = value.stride()
@@ -106,9 +108,9 @@ def _quant_batch(store: _hip.PageStore, key: Optional[torch.Tensor], value: Opti
 def quantize_into_pools(store: _hip.PageStore, key: Optional[torch.Tensor], value: Optional[torch.Tensor],
                         boost_idx: Optional[torch.Tensor], page_ids: torch.Tensor, sentinel: int,
                         value_rows: Optional[int] = None) -> None:
-    """One launch over an (outer, inner=head) grid of fp16 blocks.
+    """One launch over an (outer, inner=head) grid of fp16 or bf16 blocks.
 
-    key / value: (n_outer, n_inner, G, D) fp16 views (any strides);
+    key / value: (n_outer, n_inner, G, D) fp16 or bf16 views (any strides);
     boost_idx: (n_outer, n_inner, D) or (n_inner, D) uint8; page_ids: (n_outer,)
     int32 device tensor of destination pages.
     """
@@ -159,6 +161,12 @@ class DecodePlan:
     pools as in the layout manager; boost_idx (Hkv, D) uint8;
     sink_k/v (B, Hkv, S, D) fp16 + sink_len (B,) int32;
     tail_k/v (B, Hkv, T, D) fp16 + tail_len (B,) int32; out (B, Hq, D) fp16.
+    With a bfloat16 config, q, the sinks and the tails are bfloat16 and so
+    are the metadata pools; out stays fp16 (the reference returns fp16,
+    kernels/attention.py:189).  ``kernel`` names the split kernel the plan
+    runs ("mfma" or "generic"); a plan at the production shape that falls
+    back to the generic kernel (repeated boost ranks, bf16 or misaligned
+    buffers) warns once per process.
 
     Independent value stream (the KIVI split of the pipeline's FP16 value
     window): num_pages_v (B,) int32 value pages and tail_len_v (B,) int32
@@ -182,9 +190,9 @@ class DecodePlan:
         B, Hq, D = q.shape
         P, Hkv, D2, G4 = key_baseline.shape
         _need(D2 == D, "head_dim mismatch between q and pools")
-        _check_fp16("q", q)
+        act_dtype = _dtype16("q, sinks and tails", q, sink_k, sink_v, tail_k, tail_v)
+        meta_dtype = _dtype16("key_metadata and value_metadata", key_meta, value_meta)
         for name, t in (("sink_k", sink_k), ("sink_v", sink_v), ("tail_k", tail_k), ("tail_v", tail_v)):
-            _check_fp16(name, t)
             _need(t.dim() == 4 and t.shape[0] == B and t.shape[1] == Hkv and t.shape[3] == D
                   and (t.shape[2] == 0 or t.stride(3) == 1),
                   f"{name} must be (B, Hkv, n, D) with contiguous channels")
@@ -231,7 +239,13 @@ class DecodePlan:
             boost_unique = boost_rows_unique(boost_idx, key_boost.shape[2])
         a.flags = _hip.KITTY_DECODE_UNIQUE_BOOST_ROWS if boost_unique else 0
         a.sm_scale = float(1.0 / math.sqrt(D) if sm_scale is None else sm_scale)
+        a.meta_dtype, a.act_dtype = meta_dtype, act_dtype
         self._L = _hip.load()
+        path = ctypes.c_int32(0)
+        _hip.check(self._L.kitty_decode_path(ctypes.byref(a), ctypes.byref(path)))
+        self.kernel = "mfma" if path.value == _hip.KITTY_DECODE_PATH_MFMA else "generic"
+        if self.kernel == "generic" and D == 128 and G4 * 4 == 128 and Hq // Hkv in (4, 8, 16):
+            _warn_generic(boost_unique, act_dtype, meta_dtype)
         need = ctypes.c_size_t(0)
         _hip.check(self._L.kitty_decode_workspace_size(ctypes.byref(a), ctypes.byref(need)))
         if workspace is None or workspace.numel() * workspace.element_size() < need.value:
@@ -254,8 +268,8 @@ class DecodePlan:
         shapes and strides (a plan cached across decode steps: everything
         else it reads is device state that the steps update in place)."""
         for name, t, ref in (("q", q, self._keep[0]), ("out", out, self.out)):
-            _need(t.device == self.device and t.dtype == torch.float16 and t.shape == ref.shape
-                  and t.stride() == ref.stride(), f"{name} must match the plan's shape, strides and device")
+            _need(t.device == self.device and t.dtype == ref.dtype and t.shape == ref.shape
+                  and t.stride() == ref.stride(), f"{name} must match the plan's dtype, shape, strides and device")
         self.args.q, self.args.out = q.data_ptr(), out.data_ptr()
         try:
             _hip.check(self._L.kitty_paged_decode(ctypes.byref(self.args), _hip.stream_ptr(self.device)))
@@ -269,6 +283,24 @@ class DecodePlan:
     def run_merge(self) -> torch.Tensor:
         _hip.check(self._L.kitty_paged_decode_merge(ctypes.byref(self.args), _hip.stream_ptr(self.device)))
         return self.out
+
+
+_warned_generic = False
+
+
+def _warn_generic(boost_unique: bool, act_dtype: int, meta_dtype: int) -> None:
+    global _warned_generic
+    if _warned_generic:
+        return
+    _warned_generic = True
+    if not boost_unique:
+        why = "a boost_idx row repeats a rank below d_boost"
+    elif act_dtype == _hip.KITTY_DTYPE_BF16 or meta_dtype == _hip.KITTY_DTYPE_BF16:
+        why = "the buffers are bfloat16"
+    else:
+        why = "a pool or FP16 buffer is not 16-byte aligned"
+    warnings.warn(f"kitty paged decode runs the shape-generic kernel because {why}; at this shape it is about "
+                  "15x slower than the MFMA kernel", RuntimeWarning, stacklevel=3)
 
 
 def paged_decode(*args, **kwargs) -> torch.Tensor:

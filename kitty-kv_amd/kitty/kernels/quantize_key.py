@@ -14,7 +14,7 @@ from typing import Tuple
 import torch
 
 from .. import _hip
-from .ops import _need, quantize_into_pools
+from .ops import _dtype16, _need, quantize_into_pools
 
 
 def _key_store(D: int, G: int, D_boost: int, out_baseline, out_boost, out_scale, out_zero) -> _hip.PageStore:
@@ -22,9 +22,9 @@ def _key_store(D: int, G: int, D_boost: int, out_baseline, out_boost, out_scale,
           and out_baseline.stride(1) == 1, "out_baseline must be uint8 (D, G//4) with contiguous rows")
     _need(tuple(out_boost.shape) == (D_boost, G // 4) and out_boost.dtype == torch.uint8
           and (D_boost == 0 or out_boost.stride(1) == 1), "out_boost must be uint8 (D_boost, G//4)")
-    _need(out_scale.shape == (D,) and out_zero.shape == (D,) and out_scale.dtype == torch.float16
-          and out_zero.dtype == torch.float16 and out_scale.stride(0) == out_zero.stride(0),
-          "out_scale / out_zero must be float16 (D,) views with equal strides")
+    _need(out_scale.shape == (D,) and out_zero.shape == (D,) and out_scale.stride(0) == out_zero.stride(0),
+          "out_scale / out_zero must be (D,) views with equal strides")
+    meta_dtype = _dtype16("out_scale and out_zero", out_scale, out_zero)
     s = _hip.PageStore()
     s.key_low, s.key_low_s_row = out_baseline.data_ptr(), out_baseline.stride(0)
     s.key_high = out_boost.data_ptr() if D_boost > 0 else 0
@@ -32,14 +32,17 @@ def _key_store(D: int, G: int, D_boost: int, out_baseline, out_boost, out_scale,
     s.key_scale, s.key_zero, s.key_meta_s_chan = out_scale.data_ptr(), out_zero.data_ptr(), out_scale.stride(0)
     s.num_pages = 1
     s.num_kv_heads, s.head_dim, s.page_tokens, s.d_boost = 1, D, G, D_boost
+    s.meta_dtype = meta_dtype
     return s
 
 
 def quantize_key_page(key: torch.Tensor, boost_idx: torch.Tensor, D_boost: int, sentinel: int,
                       out_baseline: torch.Tensor, out_boost: torch.Tensor,
                       out_scale: torch.Tensor, out_zero: torch.Tensor) -> None:
-    """Quantise one (D, G) fp16 key block into pre-allocated outputs
-    (reference quantize_key.py:217-269)."""
+    """Quantise one (D, G) fp16 or bf16 key block into pre-allocated outputs
+    (reference quantize_key.py:217-269); float16 or bfloat16 out_scale /
+    out_zero receive the fp16 scale and zero point converted to their dtype,
+    as the reference's copy_ does."""
     dev = _hip.require_device(key, boost_idx, out_baseline, out_boost, out_scale, out_zero)
     D, G = key.shape
     assert G % 4 == 0, "G must be divisible by 4 for uint8 packing"

@@ -12,27 +12,29 @@ from typing import Tuple
 import torch
 
 from .. import _hip
-from .ops import _need, quantize_into_pools
+from .ops import _dtype16, _need, quantize_into_pools
 
 
 def _value_store(G: int, D: int, out_packed, out_scale, out_zero) -> _hip.PageStore:
     _need(tuple(out_packed.shape) == (G, D // 4) and out_packed.dtype == torch.uint8
           and out_packed.stride(1) == 1, "out_packed must be uint8 (G, D//4) with contiguous rows")
-    _need(out_scale.shape == (G,) and out_zero.shape == (G,) and out_scale.dtype == torch.float16
-          and out_zero.dtype == torch.float16 and out_scale.stride(0) == out_zero.stride(0),
-          "out_scale / out_zero must be float16 (G,) views with equal strides")
+    _need(out_scale.shape == (G,) and out_zero.shape == (G,) and out_scale.stride(0) == out_zero.stride(0),
+          "out_scale / out_zero must be (G,) views with equal strides")
+    meta_dtype = _dtype16("out_scale and out_zero", out_scale, out_zero)
     s = _hip.PageStore()
     s.value, s.value_s_row = out_packed.data_ptr(), out_packed.stride(0)
     s.value_scale, s.value_zero, s.value_meta_s_tok = out_scale.data_ptr(), out_zero.data_ptr(), out_scale.stride(0)
     s.num_pages = 1
     s.num_kv_heads, s.head_dim, s.page_tokens, s.d_boost = 1, D, G, 0
+    s.meta_dtype = meta_dtype
     return s
 
 
 def quantize_value_page(value: torch.Tensor, out_packed: torch.Tensor, out_scale: torch.Tensor,
                         out_zero: torch.Tensor) -> None:
-    """Quantise one (G, D) fp16 value block into pre-allocated outputs; the
-    scale / zero views may be strided (quantize_value.py:197-227)."""
+    """Quantise one (G, D) fp16 or bf16 value block into pre-allocated
+    outputs; the scale / zero views (float16 or bfloat16) may be strided
+    (quantize_value.py:197-227)."""
     dev = _hip.require_device(value, out_packed, out_scale, out_zero)
     G, D = value.shape
     assert D % 4 == 0, "head_dim D must be divisible by 4 for packing"
@@ -59,6 +61,6 @@ def dequantize_value_page_torch(packed: torch.Tensor, scale: torch.Tensor, zero_
     G, D4 = packed.shape
     out = torch.empty(G, D4 * 4, dtype=torch.float32, device=dev)
     store = _value_store(G, D4 * 4, packed, scale, zero_point)
-    _hip.check(_hip.load().kitty_dequantize_value_page(ctypes.byref(store), 0, 0, out.data_ptr(), out.stride(0), 1,
-                                                      _hip.stream_ptr(dev)))
+    _hip.check(_hip.load().kitty_dequantize_value_page(ctypes.byref(store), 0, 0, out.data_ptr(), out.stride(0),
+                                                      _hip.KITTY_OUT_F32, _hip.stream_ptr(dev)))
     return out

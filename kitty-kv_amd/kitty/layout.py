@@ -7,15 +7,16 @@ Pools (one physical page = all KV heads of one (sequence, layer, page#)):
 
     key_baseline   (P, H, D, G/4)   uint8    low 2 bits of every channel
     key_boost      (P, H, Dk, G/4)  uint8    high 2 bits of boosted channels
-    key_metadata   (P, H, 2, D)     float16  row 0 scale, row 1 zero point
+    key_metadata   (P, H, 2, D)     dtype    row 0 scale, row 1 zero point
     value_pool     (P, H, G, D/4)   uint8    4 channels per byte
-    value_metadata (P, H, G, 2)     float16  per-token (scale, zero point)
+    value_metadata (P, H, G, 2)     dtype    per-token (scale, zero point)
 
 At D = G = 128 a (page, head) record is 9,728 B (12.5% boost) or 10,240 B
 (25%); the pools are addressed with int32 page ids and 64-bit byte offsets
 in the kernels, so P may grow to the ~3.7 M pages that fill the 288 GB of an
-MI355X.  Metadata is always fp16 (the kernels read fp16 scales); a bfloat16
-config keeps bfloat16 only for the FP16 token buffers.
+MI355X.  dtype is the config's (float16 or bfloat16, layout.py:123-137); a
+bfloat16 pool holds the fp16 scale converted to bfloat16, as the reference
+copies it.
 
 Allocation is first-fit on the lowest free index, as the reference's
 ``free_mask.nonzero()[0]`` (layout.py:186-188), but O(log n) without a device
@@ -62,9 +63,9 @@ class PageCentricKVLayoutManager:
 
         self.key_baseline = torch.zeros(P, H, D, G // 4, dtype=torch.uint8, device=dev)
         self.key_boost = torch.zeros(P, H, K, G // 4, dtype=torch.uint8, device=dev)
-        self.key_metadata = torch.zeros(P, H, 2, D, dtype=torch.float16, device=dev)
+        self.key_metadata = torch.zeros(P, H, 2, D, dtype=self._torch_dtype, device=dev)
         self.value_pool = torch.zeros(P, H, G, D // 4, dtype=torch.uint8, device=dev)
-        self.value_metadata = torch.zeros(P, H, G, 2, dtype=torch.float16, device=dev)
+        self.value_metadata = torch.zeros(P, H, G, 2, dtype=self._torch_dtype, device=dev)
 
         self._num_pages_total = P
         self._high_water = 0

@@ -66,8 +66,6 @@ _FILL, _QLEN, _NPAGES, _NPAGES_V, _VLEN = 0, 1, 2, 3, 4
 class KittyInferencePipeline:
     def __init__(self, config: KittyConfig, layout: PageCentricKVLayoutManager, boost_idx_uint8: torch.Tensor,
                  num_slots: Optional[int] = None) -> None:
-        if config.dtype != "float16":
-            raise NotImplementedError("the HIP pipeline keeps FP16 buffers in float16 only")
         self.config = config
         self.layout = layout
         dev = layout.key_baseline.device
@@ -78,11 +76,12 @@ class KittyInferencePipeline:
         self.num_slots = max(1, int(num_slots or config.max_batch_size))
         self.value_capacity = R + G     # FP16 values a sequence can hold before its value spill
         n = self.num_slots
-        f16 = torch.float16
-        self._sink_k = torch.zeros(n, L, H, S, D, dtype=f16, device=dev)
-        self._sink_v = torch.zeros(n, L, H, S, D, dtype=f16, device=dev)
-        self._qbuf_k = torch.zeros(n, L, H, G, D, dtype=f16, device=dev)
-        self._vbuf = torch.zeros(n, L, H, self.value_capacity, D, dtype=f16, device=dev)
+        # the "FP16" buffers hold the config's dtype (pipeline.py:83-106)
+        self._dtype = dt = torch.float16 if config.dtype == "float16" else torch.bfloat16
+        self._sink_k = torch.zeros(n, L, H, S, D, dtype=dt, device=dev)
+        self._sink_v = torch.zeros(n, L, H, S, D, dtype=dt, device=dev)
+        self._qbuf_k = torch.zeros(n, L, H, G, D, dtype=dt, device=dev)
+        self._vbuf = torch.zeros(n, L, H, self.value_capacity, D, dtype=dt, device=dev)
         # host mirrors of the counters, (slot, layer)
         self._fill = np.zeros((n, L), np.int64)     # sink tokens written
         self._qlen = np.zeros((n, L), np.int64)     # keys in the key buffer
@@ -116,6 +115,11 @@ class KittyInferencePipeline:
             self._slot_of[seq_id] = s
             self._seq_of[s] = seq_id
         return s
+
+    @property
+    def buffer_dtype(self) -> torch.dtype:
+        """torch dtype of the sink, key and value buffers (KittyConfig.dtype)."""
+        return self._dtype
 
     def _slot0(self) -> int:
         return self._slot_of.get(0, 0)
@@ -190,8 +194,8 @@ class KittyInferencePipeline:
         slots = np.array([self.slot(s) for s in seq_ids], np.int64)
         if len(set(slots.tolist())) != len(slots):
             raise ValueError("a sequence appears twice in one push")
-        keys = keys.to(self.device, torch.float16)
-        values = values.to(self.device, torch.float16)
+        keys = keys.to(self.device, self._dtype)
+        values = values.to(self.device, self._dtype)
         l = layer_id
         fill = self._fill[slots, l]
         in_sink = fill < S
@@ -334,8 +338,8 @@ class KittyInferencePipeline:
         with every complete page of the chunk quantised straight from it."""
         cfg = self.config
         S, G, R = cfg.sink_size, cfg.q_buffer_size, cfg.local_value_window
-        keys = keys.to(self.device, torch.float16)
-        values = values.to(self.device, torch.float16)
+        keys = keys.to(self.device, self._dtype)
+        values = values.to(self.device, self._dtype)
         T = keys.shape[2]
         l = layer_id
         for i, seq in enumerate(seq_ids):

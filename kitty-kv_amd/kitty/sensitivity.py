@@ -48,13 +48,13 @@ class _ChannelAccumulator:
         dev = _hip.require_device(key)
         if self.sum_abs.device != dev:
             self.sum_abs = self.sum_abs.to(dev)
-        if key.dtype != torch.float16:
-            key = key.to(torch.float16)
+        if key.dtype not in (torch.float16, torch.bfloat16):
+            key = key.to(torch.float16)  # the kernel reads fp16 or bf16 (a model's dtype)
         if key.stride(3) != 1:
             key = key.contiguous()
         _hip.check(_hip.load().kitty_channel_abs_sum(
-            key.data_ptr(), key.stride(0), key.stride(2), key.stride(1), B, T, H, D, self.sum_abs.data_ptr(),
-            _hip.stream_ptr(dev)))
+            key.data_ptr(), key.stride(0), key.stride(2), key.stride(1), B, T, H, D, _hip.dtype_code(key, "key"),
+            self.sum_abs.data_ptr(), _hip.stream_ptr(dev)))
         self.token_count += B * T
 
     def scores(self) -> torch.Tensor:
@@ -184,6 +184,22 @@ class KittySensitivityProfiler:
         prof.boost_masks_ = torch.load(directory / "boost_masks.pt", weights_only=True)
         prof.boost_idx_uint8_ = torch.load(directory / "boost_idx.pt", weights_only=True)
         return prof
+
+    def summary(self) -> str:
+        """Human-readable summary with the reference's lines (sensitivity.py:313-332):
+        shape, boost rate and INT4 channels per head, sentinel, and the
+        largest and mean channel score once computed."""
+        cfg = self.config
+        if self.scores_ is None:
+            return "KittySensitivityProfiler — not yet computed."
+        return "\n".join([
+            "KittySensitivityProfiler Summary",
+            f"  Layers: {cfg.num_layers}, KV Heads: {cfg.num_kv_heads}, Head Dim: {cfg.head_dim}",
+            f"  Boost rate: {cfg.boost_rate:.1%} → {cfg.d_boost} INT4 channels/head",
+            f"  Sentinel value: {cfg.sentinel}",
+            f"  Max channel score: {self.scores_.max().item():.4f}",
+            f"  Mean channel score: {self.scores_.mean().item():.4f}",
+        ])
 
     @property
     def boost_masks(self) -> torch.Tensor:

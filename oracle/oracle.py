@@ -176,10 +176,21 @@ def paged_attention(q, page_list: Sequence[int], key_baseline, key_boost, key_me
 
 # ------------------------------------------------- numpy restatements
 
+def _f32(x) -> np.ndarray:
+    """fp16 arrays and fp32 arrays (e.g. bf16 values from bf16_to_f32) as
+    fp32, exactly; any other dtype is taken as fp16 data, as the callers'
+    fp16 paths always did."""
+    a = np.asarray(x)
+    if a.dtype == np.float32:
+        return a
+    return np.asarray(a, np.float16).astype(np.float32)
+
+
 def quantize_key_np(key: np.ndarray, boost_idx: np.ndarray, d_boost: int, sentinel: int):
     """Vectorised numpy restatement of ``quantize_key_page_torch``
-    (kitty/kernels/quantize_key.py:69-124); same outputs as :func:`quantize_key`."""
-    x = np.asarray(key, np.float16).astype(np.float32)
+    (kitty/kernels/quantize_key.py:69-124); same outputs as :func:`quantize_key`.
+    key: fp16 data, or fp32 values of bf16 data (``key.float()``, :69)."""
+    x = _f32(key)
     D, G = x.shape
     boosted = np.asarray(boost_idx).astype(np.int64) < sentinel
     mn = x.min(axis=1)
@@ -202,13 +213,14 @@ def quantize_key_np(key: np.ndarray, boost_idx: np.ndarray, d_boost: int, sentin
         if bi[d] < d_boost:
             for i in range(4):
                 thigh[bi[d]] |= (hi[d, i::4] << (2 * i)).astype(np.uint8)
-    return t2b, thigh, s.astype(np.float16), zp.astype(np.float16)
+    with np.errstate(over="ignore"):          # fp16 overflow gives inf, as torch's .to(float16)
+        return t2b, thigh, s.astype(np.float16), zp.astype(np.float16)
 
 
 def quantize_value_np(value: np.ndarray):
     """Vectorised numpy restatement of ``quantize_value_page_torch``
-    (kitty/kernels/quantize_value.py:58-90)."""
-    v = np.asarray(value, np.float16).astype(np.float32)
+    (kitty/kernels/quantize_value.py:58-90); value as in quantize_key_np."""
+    v = _f32(value)
     G, D = v.shape
     mn = v.min(axis=1)
     mx = v.max(axis=1)
@@ -221,7 +233,8 @@ def quantize_value_np(value: np.ndarray):
     packed = np.zeros((G, D // 4), np.uint8)
     for i in range(4):
         packed |= (c[:, i::4] << (2 * i)).astype(np.uint8)
-    return packed, s.astype(np.float16), zp.astype(np.float16)
+    with np.errstate(over="ignore"):
+        return packed, s.astype(np.float16), zp.astype(np.float16)
 
 
 def dequantize_key_np(t2b, thigh, scale, zero, boost_idx, d_boost: int) -> np.ndarray:
@@ -235,8 +248,8 @@ def dequantize_key_np(t2b, thigh, scale, zero, boost_idx, d_boost: int) -> np.nd
         if bi[d] < d_boost:
             hi[d] = ((np.asarray(thigh, np.uint8)[bi[d]][:, None] >> shifts) & 3).reshape(-1)
     xq = (lo | (hi << 2)).astype(np.float32)
-    s = np.asarray(scale, np.float16).astype(np.float32)[:, None]
-    z = np.asarray(zero, np.float16).astype(np.float32)[:, None]
+    s = _f32(scale)[:, None]
+    z = _f32(zero)[:, None]
     return ((xq - z) * s).astype(np.float32)
 
 
@@ -245,8 +258,8 @@ def dequantize_value_np(packed, scale, zero) -> np.ndarray:
     G, D4 = packed.shape
     shifts = np.array([0, 2, 4, 6], np.uint8)
     c = ((packed[:, :, None] >> shifts) & 3).reshape(G, D4 * 4).astype(np.float32)
-    s = np.asarray(scale, np.float16).astype(np.float32)[:, None]
-    z = np.asarray(zero, np.float16).astype(np.float32)[:, None]
+    s = _f32(scale)[:, None]
+    z = _f32(zero)[:, None]
     return ((c - z) * s).astype(np.float32)
 
 
@@ -259,16 +272,16 @@ def dequantized_kv(page_list, key_baseline, key_boost, key_meta, value_pool, val
     for h in range(H):
         kp, vp_ = [], []
         if sink_k.shape[1] > 0:
-            kp.append(np.asarray(sink_k[h], np.float16).astype(np.float32))
-            vp_.append(np.asarray(sink_v[h], np.float16).astype(np.float32))
+            kp.append(_f32(sink_k[h]))
+            vp_.append(_f32(sink_v[h]))
         for p in page_list:
             kp.append(dequantize_key_np(key_baseline[p, h], key_boost[p, h], key_meta[p, h, 0],
                                         key_meta[p, h, 1], boost_idx[h], d_boost).T)
             vp_.append(dequantize_value_np(value_pool[p, h], value_meta[p, h, :, 0],
                                            value_meta[p, h, :, 1]))
         if tail_k.shape[1] > 0:
-            kp.append(np.asarray(tail_k[h], np.float16).astype(np.float32))
-            vp_.append(np.asarray(tail_v[h], np.float16).astype(np.float32))
+            kp.append(_f32(tail_k[h]))
+            vp_.append(_f32(tail_v[h]))
         Ks.append(np.concatenate(kp, 0) if kp else np.zeros((0, D), np.float32))
         Vs.append(np.concatenate(vp_, 0) if vp_ else np.zeros((0, D), np.float32))
     return Ks, Vs
@@ -307,7 +320,7 @@ def paged_attention_kv(q, key_pages, value_pages, key_baseline, key_boost, key_m
                              boost_idx, d_boost, sink_k, sink_v, tail_k, tail_v)
     g = num_q_heads // num_kv_heads
     out = np.zeros((num_q_heads, head_dim), np.float64)
-    qd = np.asarray(q, np.float16).astype(np.float64)
+    qd = _f32(q).astype(np.float64)
     for qh in range(num_q_heads):
         K, V = Ks[qh // g].astype(np.float64), Vs[qh // g].astype(np.float64)
         if K.shape[0] == 0:
@@ -316,3 +329,42 @@ def paged_attention_kv(q, key_pages, value_pages, key_baseline, key_boost, key_m
         p = np.exp(s - s.max())
         out[qh] = (p / p.sum()) @ V
     return out.astype(np.float16)
+
+
+# ---------------------------------------------------------------- bf16
+# KittyConfig.dtype = "bfloat16" (kitty/config.py:76): buffers and metadata
+# pools in bf16.  The quantisers still return fp16 scales and zero points,
+# which the launchers copy into the bf16 pool views (quantize_key.py:121-122,
+# 263-269; quantize_value.py:90, 223-227): a bf16 pool holds bf16(fp16(x)).
+# bf16 data travels as uint16 bit patterns (numpy has no bf16 type).
+
+def bf16_to_f32(bits) -> np.ndarray:
+    """bf16 bit patterns -> fp32 values (exact)."""
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def f32_to_bf16(x) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even, NaN -> 0x7FC0
+    (torch's .to(torch.bfloat16); pinned against torch in tests)."""
+    u = np.ascontiguousarray(np.asarray(x, np.float32)).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, np.uint16(0x7FC0), r).astype(np.uint16)
+
+
+def meta_bf16(x_f16) -> np.ndarray:
+    """An fp16 scale or zero point as a bf16 pool stores it: bf16(fp16(x))."""
+    return f32_to_bf16(np.asarray(x_f16, np.float16).astype(np.float32))
+
+
+def quantize_key_bf16(key_bits, boost_idx, d_boost: int, sentinel: int):
+    """bf16 key block (D, G) -> (t2b, thigh, scale, zero) with scale / zero as
+    the bf16 bit patterns a bf16 key_metadata pool holds."""
+    t2b, thigh, s, z = quantize_key_np(bf16_to_f32(key_bits), boost_idx, d_boost, sentinel)
+    return t2b, thigh, meta_bf16(s), meta_bf16(z)
+
+
+def quantize_value_bf16(value_bits):
+    """bf16 value block (G, D) -> (packed, scale, zero), scale / zero as bf16 bits."""
+    packed, s, z = quantize_value_np(bf16_to_f32(value_bits))
+    return packed, meta_bf16(s), meta_bf16(z)

@@ -46,6 +46,20 @@ def test_save_load_formats(tmp_path):
     assert torch.equal(back.boost_idx_uint8, prof.boost_idx_uint8) and torch.equal(back.scores_, prof.scores_)
 
 
+def test_summary_lines():
+    cfg = KittyConfig(num_layers=2, num_kv_heads=2, head_dim=16, boost_rate=0.25, device="cpu")
+    prof = KittySensitivityProfiler(cfg)
+    assert prof.summary() == "KittySensitivityProfiler — not yet computed."
+    prof.scores_ = torch.tensor([0.5, 1.5, 4.0, 2.0]).reshape(1, 1, 4).expand(2, 2, 4).contiguous()
+    lines = prof.summary().split("\n")
+    assert lines[0] == "KittySensitivityProfiler Summary"
+    assert lines[1] == "  Layers: 2, KV Heads: 2, Head Dim: 16"
+    assert lines[2] == "  Boost rate: 25.0% → 4 INT4 channels/head"
+    assert lines[3] == "  Sentinel value: 5"
+    assert lines[4] == "  Max channel score: 4.0000"
+    assert lines[5] == "  Mean channel score: 2.0000"
+
+
 def test_accumulation_needs_a_rocm_device():
     cfg = KittyConfig(num_layers=1, num_kv_heads=2, head_dim=16, device="cpu")
     prof = KittySensitivityProfiler(cfg)
