@@ -23,6 +23,10 @@ torch's ``scaled_dot_product_attention`` on the oracle's dequantised K/V.
 reduction to the C paged attention when both streams hold the same pages, by
 the equivalence of a value page and its dequantised rows in the FP16 value
 tail, and by SDPA on the assembled streams.
+The bf16 helpers (``f32_to_bf16``, ``quantize_key_bf16``,
+``quantize_value_bf16``; KittyConfig.dtype = "bfloat16") are pinned in
+tests/test_bf16.py: the rounding equals torch's ``.to(torch.bfloat16)``, and
+blocks fp16 also holds reduce to the fp16 path with bf16(fp16(x)) metadata.
 Only the sign of a zero zero-point and the reference's fp32 summation order
 are unpinned; both are compared by value / within tolerance.
 """
