@@ -11,44 +11,75 @@ namespace kitty {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-// One workgroup per sequence, 64 threads; H x D fp16 of K and of V.
+// One workgroup per sequence, 64 threads; H x D 16-bit values of K and of V
+// (fp16 or bf16: rows are copied bit for bit).  The kernel is one basic block
+// up to its last stores, so the token's first kAppendRows x 64 16-byte
+// vectors (all of them at H x D = 8 x 128), the slot id, and then the
+// counters are loaded back to back: a launch costs two memory round trips.
+// The row loads are unconditional (a lane past the end reloads the last
+// vector and writes it back to its own place), and the row stores go through
+// buffer descriptors whose record count is 0 when nothing may be written, so
+// the hardware drops them; a store under a branch would let the compiler sink
+// the loads feeding it behind the counter loads.
+constexpr int kAppendRows = 2;
+constexpr int kBufferWord3 = 0x00020000;  // raw (untyped) buffer, gfx9 family
+
 __global__ __launch_bounds__(64) void append_tokens_kernel(kitty_append_args a)
 {
     const int b = blockIdx.x;
-    const int slot = a.slots[b];
-    if (slot < 0 || slot >= a.num_slots)
-        return;
-    const int fill = a.sink_fill[slot], qlen = a.buf_len[slot];
-    const bool to_sink = fill < a.sink_size;
-    const bool own_values = a.val_len != nullptr;
-    const int vlen = own_values ? a.val_len[slot] : qlen;
-    if (!to_sink && (qlen >= a.buf_tokens || (own_values && vlen >= a.val_tokens))) {
-        // the caller did not spill a full buffer: flag it, write nothing
-        if (threadIdx.x == 0)
-            a.overflow[b] = 1;
-        return;
-    }
-    const int kpos = to_sink ? fill : qlen;
-    uint16_t *dk = to_sink ? a.sink_k : a.buf_k;
-    const kitty_slot_layout &KL = to_sink ? a.sink_layout : a.buf_layout;
-    const int vpos = to_sink ? fill : vlen;
-    uint16_t *dv = to_sink ? a.sink_v : (own_values ? a.val_buf : a.buf_v);
-    const kitty_slot_layout &VL = to_sink ? a.sink_layout : (own_values ? a.val_layout : a.buf_layout);
     const int vec = a.head_dim / 8;  // 16-byte vectors per head row
-    for (int e = threadIdx.x; e < a.num_kv_heads * vec; e += blockDim.x) {
-        const int h = e / vec, c = (e - h * vec) * 8;
-        const int64_t src_k = b * a.key_s_seq + h * a.key_s_head + c;
-        const int64_t src_v = b * a.value_s_seq + h * a.value_s_head + c;
-        *(u32x4 *)(dk + slot * KL.s_slot + h * KL.s_head + kpos * KL.s_tok + c) = *(const u32x4 *)(a.key + src_k);
-        *(u32x4 *)(dv + slot * VL.s_slot + h * VL.s_head + vpos * VL.s_tok + c) = *(const u32x4 *)(a.value + src_v);
+    const int n = a.num_kv_heads * vec;
+    u32x4 kr[kAppendRows], vr[kAppendRows];
+    int hd[kAppendRows], ch[kAppendRows];
+#pragma unroll
+    for (int i = 0; i < kAppendRows; ++i) {
+        const int e = min((int)threadIdx.x + i * 64, n - 1);
+        hd[i] = e / vec;
+        ch[i] = (e - hd[i] * vec) * 8;
+        kr[i] = *(const u32x4 *)(a.key + b * a.key_s_seq + hd[i] * a.key_s_head + ch[i]);
+        vr[i] = *(const u32x4 *)(a.value + b * a.value_s_seq + hd[i] * a.value_s_head + ch[i]);
     }
-    if (threadIdx.x == 0) {
-        if (to_sink) {
-            a.sink_fill[slot] = fill + 1;
+    const int slot = a.slots[b];
+    const bool valid = slot >= 0 && slot < a.num_slots;
+    const int s = valid ? slot : 0;
+    const bool own_values = a.val_len != nullptr;
+    const int fill = a.sink_fill[s], qlen = a.buf_len[s];
+    const int vlen = (own_values ? a.val_len : a.buf_len)[s];
+    const bool to_sink = fill < a.sink_size;
+    // the caller did not spill a full buffer: flag it, write nothing
+    const bool full = !to_sink && (qlen >= a.buf_tokens || (own_values && vlen >= a.val_tokens));
+    const bool write = valid && !full;
+    const kitty_slot_layout KL = to_sink ? a.sink_layout : a.buf_layout;
+    const kitty_slot_layout VL = to_sink ? a.sink_layout : (own_values ? a.val_layout : a.buf_layout);
+    uint16_t *dk = (to_sink ? a.sink_k : a.buf_k) + s * KL.s_slot + (to_sink ? fill : qlen) * KL.s_tok;
+    uint16_t *dv = (to_sink ? a.sink_v : (own_values ? a.val_buf : a.buf_v)) + s * VL.s_slot +
+                   (to_sink ? fill : vlen) * VL.s_tok;
+    const int records = __builtin_amdgcn_readfirstlane(write ? -1 : 0);  // uniform: keep the descriptor in SGPRs
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc(dk, 0, records, kBufferWord3);
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc(dv, 0, records, kBufferWord3);
+#pragma unroll
+    for (int i = 0; i < kAppendRows; ++i) {
+        // byte offsets below 2^31: the host checks (H - 1) * s_head + D
+        __builtin_amdgcn_raw_buffer_store_b128(kr[i], rk, (int)(hd[i] * KL.s_head + ch[i]) * 2, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(vr[i], rv, (int)(hd[i] * VL.s_head + ch[i]) * 2, 0, 0);
+    }
+    if (write) {
+        for (int e = threadIdx.x + kAppendRows * 64; e < n; e += blockDim.x) {   // H x D past 8 x 128
+            const int h = e / vec, c = (e - h * vec) * 8;
+            *(u32x4 *)(dk + h * KL.s_head + c) = *(const u32x4 *)(a.key + b * a.key_s_seq + h * a.key_s_head + c);
+            *(u32x4 *)(dv + h * VL.s_head + c) =
+                *(const u32x4 *)(a.value + b * a.value_s_seq + h * a.value_s_head + c);
+        }
+    }
+    if (threadIdx.x == 0 && valid) {
+        if (full) {
+            a.overflow[b] = 1;
+        } else if (to_sink) {
+            a.sink_fill[s] = fill + 1;
         } else {
-            a.buf_len[slot] = qlen + 1;
+            a.buf_len[s] = qlen + 1;
             if (own_values)
-                a.val_len[slot] = vlen + 1;
+                a.val_len[s] = vlen + 1;
         }
     }
 }
@@ -82,6 +113,11 @@ extern "C" int kitty_append_tokens(const kitty_append_args *args, kitty_stream_t
     for (int64_t s : strides)
         if (s % 8)
             return fail(KITTY_E_INVALID, "append strides must be multiples of 8 elements (16-byte rows)");
+    // the kernel addresses a token's H x D block of a buffer with 32-bit byte offsets
+    const int64_t head_strides[] = {a.sink_layout.s_head, a.buf_layout.s_head, own_values ? a.val_layout.s_head : 0};
+    for (int64_t s : head_strides)
+        if (s < 0 || (a.num_kv_heads - 1) * s + a.head_dim >= (int64_t(1) << 30))
+            return fail(KITTY_E_INVALID, "append buffer head stride must be non-negative with (H-1)*s_head+D < 2^30");
     if (!al16(a.key) || !al16(a.value) || !al16(a.buf_k) || !al16(own_values ? a.val_buf : a.buf_v) ||
         (a.sink_size > 0 && (!al16(a.sink_k) || !al16(a.sink_v))))
         return fail(KITTY_E_INVALID, "append buffers must be 16-byte aligned");
