@@ -21,10 +21,11 @@
 // a zero row instead of branching, and the destination page id is looked up
 // after the loads are issued.
 //
-// Arithmetic is that of quantize.h (bit-exact with the reference); the codes
-// use the multiply-by-reciprocal of rint_quot below, which returns the same
-// integer as rint of the correctly rounded quotient, checked eight elements
-// at a time (rint_quot8).
+// Arithmetic is that of quantize.h (bit-exact with the reference).  The
+// zero points use the multiply-by-reciprocal of rint_quot below, which
+// returns the same integer as rint of the correctly rounded quotient; the
+// codes use the same argument in the fused form of magic_round8, eight
+// elements at a time, with the code left in the low bits of a float.
 #include "quantize.h"
 
 #pragma clang fp contract(off)
@@ -51,10 +52,10 @@ __device__ __forceinline__ unsigned as_u(h2 v) { return __builtin_bit_cast(unsig
 __device__ __forceinline__ h2 hmin(h2 a, h2 b) { return __builtin_elementwise_min(a, b); }
 __device__ __forceinline__ h2 hmax(h2 a, h2 b) { return __builtin_elementwise_max(a, b); }
 
-__device__ __forceinline__ float chan(const u32x4 &v, int c)
+__device__ __forceinline__ _Float16 chan(const u32x4 &v, int c)
 {
     const unsigned w = v[c >> 1];
-    return h2f((uint16_t)((c & 1) ? (w >> 16) : (w & 0xffffu)));
+    return __builtin_bit_cast(_Float16, (uint16_t)((c & 1) ? (w >> 16) : (w & 0xffffu)));
 }
 
 template <int CTRL>
@@ -81,29 +82,46 @@ __device__ __forceinline__ float rint_quot(float x, float s, float rs)
     return n;
 }
 
-// rint_quot of eight elements that share (s, rs), with one branch for the
-// eight: when any of them lies near a half-integer, all eight are recomputed
-// from the correctly rounded quotient (which the fast path only reproduces).
-__device__ __forceinline__ void rint_quot8(const float (&x)[8], float s, float rs, float (&n)[8])
+// Codes of eight fp16 elements that share (s, rs = v_rcp(s), z), as floats
+// whose bit patterns carry the code: kC + c with c = clamp(rint(x / s) + z,
+// 0, mq) in the low bits (2^23 <= kC + c < 2^24, one unit per ulp), the
+// quotient correctly rounded as in the reference.
+//
+// t = fma(x, rs, kC + z) rounds p + z + kC to an integer in one step, p = x *
+// rs exact (inside the fma).  p is within 2^-18 * 1.5 of the correctly
+// rounded quotient q while |q| < 32 (the argument of rint_quot), and
+// e = fma(x, rs, -(t - kC - z)) is p - rint(p) to 2^-25, so when no |e|
+// exceeds 0.5 - 2^-14 every p is at least 2^-14 - 2^-25 > 2^-17 from a
+// half-integer: rint(p) = rint(q), and t = kC + z + rint(q) whenever that
+// lies in [2^23, 2^24).  Below 2^23, p + z < 0 and t clamps to code 0, which
+// is the clamped code of rint(q) + z <= 0; at or above 2^24, p + z >= 2^23
+// and t clamps to mq, as does rint(q) + z.  Outside |q| < 32 the clamped
+// codes agree for the same reason as in rint_quot.  A group with an element
+// near a half-integer recomputes all eight from the correctly rounded
+// quotient.  The fp16 operands are read in place (v_fma_mix_f32).
+constexpr float kC = 0x1p23f;
+
+__device__ __forceinline__ void magic_round8(const _Float16 (&x)[8], float s, float rs, float z, float (&t)[8])
 {
-    float dev = 0.0f;  // largest |y - rint(y)| of the eight
+    const float cz = kC + z;  // exact: z is an integer in [0, 15]
+    float dev = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float y = x[e] * rs;
-        n[e] = __builtin_rintf(y);
-        dev = __builtin_fmaxf(dev, __builtin_fabsf(y - n[e]));
+        t[e] = __builtin_fmaf((float)x[e], rs, cz);
+        dev = __builtin_fmaxf(dev, __builtin_fabsf(__builtin_fmaf((float)x[e], rs, -(t[e] - cz))));
     }
     if (__builtin_expect(dev > 0.5f - 0x1p-14f, 0)) {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-            n[e] = __builtin_rintf(x[e] / s);
+            t[e] = __builtin_rintf((float)x[e] / s) + cz;
     }
 }
 
-// clamp(n + z, 0, mq) -> code; n and z are small integers, so v_med3 is exact.
-__device__ __forceinline__ unsigned code_of(float n, float z, float mq)
+// The clamped code of t from magic_round8 as the low bits of a word:
+// kC + clamp(t - kC, 0, mq) has the bit pattern 0x4B000000 | code.
+__device__ __forceinline__ unsigned code_bits(float t, float mq)
 {
-    return (unsigned)__builtin_amdgcn_fmed3f(n + z, 0.0f, mq);
+    return __builtin_bit_cast(unsigned, __builtin_amdgcn_fmed3f(t, kC, kC + mq));
 }
 
 // 256 bytes of zeros: the rows of a block past `rows_valid` are loaded from
@@ -241,15 +259,16 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
     read8(lds, kParOff + 2048 + 32 * cg, hr);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-        float x[8], n[8];
+        _Float16 x[8];
+        float t[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k)
             x[k] = chan(r[k], c);
-        rint_quot8(x, s[c], rs[c], n);
+        magic_round8(x, s[c], rs[c], z[c], t);
         unsigned lo = 0, hi = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {                                  // :95-103
-            const unsigned q = code_of(n[k], z[c], mq[c]);
+            const unsigned q = code_bits(t[k], mq[c]);
             lo |= (q & 3u) << (2 * k);
             hi |= ((q >> 2) & 3u) << (2 * k);
         }
@@ -326,15 +345,19 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
     read8(lds, kParOff + 1024 + 32 * tt, z);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        float x[8], n[8];
+        _Float16 x[8];
+        float t[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c)
             x[c] = chan(r[k], c);
-        rint_quot8(x, s[k], rs[k], n);
-        unsigned bits = 0;
+        magic_round8(x, s[k], rs[k], z[k], t);
+        // :74-88, channel 4j+i at byte j bits 2i; a code is at most 3, and the
+        // words' constant high bits land at bit 24 and above: the low 16 bits
+        // are the packed codes
+        unsigned bits = code_bits(t[0], 3.0f);
 #pragma unroll
-        for (int c = 0; c < 8; ++c)                                    // :74-88, channel 4j+i at byte j bits 2i
-            bits |= code_of(n[c], z[k], 3.0f) << (2 * c);
+        for (int c = 1; c < 8; ++c)
+            bits |= code_bits(t[c], 3.0f) << (2 * c);
         *(uint16_t *)(lds + tile_off(8 * tt + k) + 2 * cg) = (uint16_t)bits;
     }
     __syncthreads();
