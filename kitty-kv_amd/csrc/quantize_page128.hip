@@ -24,7 +24,7 @@
 // Arithmetic is that of quantize.h (bit-exact with the reference).  The
 // zero points use the multiply-by-reciprocal of rint_quot below, which
 // returns the same integer as rint of the correctly rounded quotient; the
-// codes use the same argument in the fused form of magic_round8, eight
+// codes use the same argument in the fused form of magic_fast8x8, eight
 // elements at a time, with the code left in the low bits of a float.
 #include "quantize.h"
 
@@ -82,10 +82,10 @@ __device__ __forceinline__ float rint_quot(float x, float s, float rs)
     return n;
 }
 
-// Codes of eight fp16 elements that share (s, rs = v_rcp(s), z), as floats
-// whose bit patterns carry the code: kC + c with c = clamp(rint(x / s) + z,
-// 0, mq) in the low bits (2^23 <= kC + c < 2^24, one unit per ulp), the
-// quotient correctly rounded as in the reference.
+// Codes of eight fp16 elements that share (s, rs = v_rcp(s), z): floats t
+// that code_bits clamps to kC + c, c = clamp(rint(x / s) + z, 0, mq) with
+// the quotient correctly rounded as in the reference; kC + c lies in
+// [2^23, 2^24), one unit per ulp, so its low bits are c.
 //
 // t = fma(x, rs, kC + z) rounds p + z + kC to an integer in one step, p = x *
 // rs exact (inside the fma).  p is within 2^-18 * 1.5 of the correctly
@@ -99,25 +99,64 @@ __device__ __forceinline__ float rint_quot(float x, float s, float rs)
 // codes agree for the same reason as in rint_quot.  A group with an element
 // near a half-integer recomputes all eight from the correctly rounded
 // quotient.  The fp16 operands are read in place (v_fma_mix_f32).
+//
+// The kernels run the fast step of all eight groups of a thread first and
+// the (rarely taken) exact recomputations after.
 constexpr float kC = 0x1p23f;
+constexpr float kNearHalf = 0.5f - 0x1p-14f;
 
-__device__ __forceinline__ void magic_round8(const _Float16 (&x)[8], float s, float rs, float z, float (&t)[8])
+// Fast step for a thread's eight groups of eight, x(g, e) the fp16 element:
+// t[g][e] = fma(x, rs[g], cz[g]) (cz = kC + z) and dev[g] = the group's
+// largest |p - rint(p)|.  The work runs in phases (every t, every t - cz,
+// every e, the maxima) with scheduling barriers between them, four groups at
+// a time: a phase is 32 independent operations, so no result is read by the
+// instruction after the one that wrote it (a v_fma_mix_f32 result read at
+// once costs a wait state) and the groups' latencies overlap.
+template <typename X>
+__device__ __forceinline__ void magic_fast8x8(X x, const float (&rs)[8], const float (&cz)[8], float (&t)[8][8],
+                                              float (&dev)[8])
 {
-    const float cz = kC + z;  // exact: z is an integer in [0, 15]
-    float dev = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        t[e] = __builtin_fmaf((float)x[e], rs, cz);
-        dev = __builtin_fmaxf(dev, __builtin_fabsf(__builtin_fmaf((float)x[e], rs, -(t[e] - cz))));
-    }
-    if (__builtin_expect(dev > 0.5f - 0x1p-14f, 0)) {
+    for (int h = 0; h < 8; h += 4) {
+        float n[4][8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            t[e] = __builtin_rintf((float)x[e] / s) + cz;
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                t[h + g][e] = __builtin_fmaf((float)x(h + g, e), rs[h + g], cz[h + g]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                n[g][e] = t[h + g][e] - cz[h + g];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                n[g][e] = __builtin_fmaf((float)x(h + g, e), rs[h + g], -n[g][e]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                d = __builtin_fmaxf(d, __builtin_fabsf(n[g][e]));
+            dev[h + g] = d;
+        }
     }
 }
 
-// The clamped code of t from magic_round8 as the low bits of a word:
+// Exact step for a group whose dev exceeds kNearHalf.
+__device__ __forceinline__ void magic_exact8(const _Float16 (&x)[8], float s, float cz, float (&t)[8])
+{
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        t[e] = __builtin_rintf((float)x[e] / s) + cz;  // cz exact: z is an integer in [0, 15]
+}
+
+// The clamped code of t from magic_fast8x8 / magic_exact8 as the low bits of a word:
 // kC + clamp(t - kC, 0, mq) has the bit pattern 0x4B000000 | code.
 __device__ __forceinline__ unsigned code_bits(float t, float mq)
 {
@@ -225,6 +264,10 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
 
     float *ps = (float *)(lds + kParOff), *prs = ps + 128, *pz = ps + 256, *pmq = ps + 384;
     int *phr = (int *)(ps + 512);
+    // the channel's stored scale / zero point, written with the page at the
+    // end: a store here would make the code loop wait for it (its address
+    // registers get reused, and reuse waits for every outstanding store)
+    uint16_t meta_s = 0, meta_z = 0;
     if (tid < 128) {  // channel d = tid
         const uint16_t *rmn = (const uint16_t *)(lds + kRedOff), *rmx = rmn + 512;
         float cmn = h2f(rmn[tid]), cmx = h2f(rmx[tid]);
@@ -242,11 +285,8 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
         pz[tid] = z;
         pmq[tid] = mq;
         phr[tid] = b < Dk ? b : -1;                                    // :113-116
-        if (ok) {
-            const int64_t m = page * st.key_meta_s_page + i * st.key_meta_s_head + tid;
-            st.key_scale[m] = f2h(s);                                  // :121-122
-            st.key_zero[m] = f2h(z);
-        }
+        meta_s = f2h(s);                                               // :121-122
+        meta_z = f2h(z);
     }
     __syncthreads();
 
@@ -257,18 +297,27 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
     read8(lds, kParOff + 1024 + 32 * cg, z);
     read8(lds, kParOff + 1536 + 32 * cg, mq);
     read8(lds, kParOff + 2048 + 32 * cg, hr);
+    float t[8][8], dev[8], cz[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+        cz[c] = kC + z[c];
+    magic_fast8x8([&](int c, int k) { return chan(r[k], c); }, rs, cz, t, dev);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-        _Float16 x[8];
-        float t[8];
+        if (__builtin_expect(dev[c] > kNearHalf, 0)) {
+            _Float16 x[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            x[k] = chan(r[k], c);
-        magic_round8(x, s[c], rs[c], z[c], t);
+            for (int k = 0; k < 8; ++k)
+                x[k] = chan(r[k], c);
+            magic_exact8(x, s[c], cz[c], t[c]);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
         unsigned lo = 0, hi = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {                                  // :95-103
-            const unsigned q = code_bits(t[k], mq[c]);
+            const unsigned q = code_bits(t[c][k], mq[c]);
             lo |= (q & 3u) << (2 * k);
             hi |= ((q >> 2) & 3u) << (2 * k);
         }
@@ -284,6 +333,11 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
     if (tid < 2 * Dk)
         *(u32x4 *)(st.key_high + page * st.key_high_s_page + i * st.key_high_s_head + 16 * tid) =
             *(const u32x4 *)(lds + kHighOff + 16 * tid);
+    if (tid < 128) {
+        const int64_t m = page * st.key_meta_s_page + i * st.key_meta_s_head + tid;
+        st.key_scale[m] = meta_s;
+        st.key_zero[m] = meta_z;
+    }
 }
 
 // ----------------------------------------------------------------- values
@@ -343,21 +397,30 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
     read8(lds, kParOff + 32 * tt, s);
     read8(lds, kParOff + 512 + 32 * tt, rs);
     read8(lds, kParOff + 1024 + 32 * tt, z);
+    float t[8][8], dev[8], cz[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        cz[k] = kC + z[k];
+    magic_fast8x8([&](int k, int c) { return chan(r[k], c); }, rs, cz, t, dev);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        _Float16 x[8];
-        float t[8];
+        if (__builtin_expect(dev[k] > kNearHalf, 0)) {
+            _Float16 x[8];
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
-            x[c] = chan(r[k], c);
-        magic_round8(x, s[k], rs[k], z[k], t);
+            for (int c = 0; c < 8; ++c)
+                x[c] = chan(r[k], c);
+            magic_exact8(x, s[k], cz[k], t[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
         // :74-88, channel 4j+i at byte j bits 2i; a code is at most 3, and the
         // words' constant high bits land at bit 24 and above: the low 16 bits
         // are the packed codes
-        unsigned bits = code_bits(t[0], 3.0f);
+        unsigned bits = code_bits(t[k][0], 3.0f);
 #pragma unroll
         for (int c = 1; c < 8; ++c)
-            bits |= code_bits(t[c], 3.0f) << (2 * c);
+            bits |= code_bits(t[k][c], 3.0f) << (2 * c);
         *(uint16_t *)(lds + tile_off(8 * tt + k) + 2 * cg) = (uint16_t)bits;
     }
     __syncthreads();
