@@ -20,6 +20,8 @@
 
 namespace kitty {
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kGenThreads = 256;
 
 // LDS for one generic workgroup, carved from dynamic shared memory.
@@ -351,6 +353,79 @@ __device__ __forceinline__ void merge_one_pass(const DecodeParams &p, int64_t ro
     }
 }
 
+// Merge of NS <= 4 K partials of D = 128 channels in one round trip: lane
+// group g = lane / 16 takes partials g, g + 4, g + 8, ... and lane c = lane
+// % 16 of the group channels 8c .. 8c + 7, so one 16-byte load per lane
+// covers four partial rows (two per row and lane), every (m, l) and O load
+// issued together (indices past NS clamp to the last partial and weigh 0).
+// The weighted sums of the four groups are added across lanes 16 and 32
+// apart.  Configs 3 and 5 (17 and 66 partials per row) take 12 and 60 loads
+// per lane where a float2 per lane and partial took 33 and 130.
+template <int K>
+__device__ __forceinline__ void merge_quads(const DecodeParams &p, int64_t row0, int64_t rstep, int NS, uint16_t *o)
+{
+    const int lane = threadIdx.x, g = lane >> 4, c = lane & 15;
+    const float ninf = -__builtin_inff();
+    float4 va[K], vb[K];
+    float2 ml[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        const int64_t row = row0 + (int64_t)min(g + 4 * i, NS - 1) * rstep;
+        const float *src = p.ws_o + row * 128 + 8 * c;
+        va[i] = *(const float4 *)src;
+        vb[i] = *(const float4 *)(src + 4);
+        ml[i] = *(const float2 *)(p.ws_ml + 2 * row);
+    }
+    float mloc = ninf;
+    bool nanl = false;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        if (g + 4 * i < NS) {
+            mloc = fmaxf(mloc, ml[i].x);
+            nanl |= ml[i].x != ml[i].x;
+        }
+    }
+    const float M = wave_max(mloc);
+    const bool nan = wave_max(nanl ? 1.0f : 0.0f) > 0.0f;
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, lsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        const float w = g + 4 * i < NS && ml[i].x != ninf && M != ninf ? exp2f(ml[i].x - M) : 0.0f;
+        lsum += w * ml[i].y;
+        acc[0] += w * va[i].x;
+        acc[1] += w * va[i].y;
+        acc[2] += w * va[i].z;
+        acc[3] += w * va[i].w;
+        acc[4] += w * vb[i].x;
+        acc[5] += w * vb[i].y;
+        acc[6] += w * vb[i].z;
+        acc[7] += w * vb[i].w;
+    }
+#pragma unroll
+    for (int off = 16; off <= 32; off *= 2) {
+        lsum += __shfl_xor(lsum, off);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            acc[e] += __shfl_xor(acc[e], off);
+    }
+    if (g != 0)
+        return;
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;  // no tokens -> zeros (attention.py:180-182)
+    uint16_t h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        h[e] = f2h(nan ? __builtin_nanf("") : acc[e] * inv);
+    uint16_t *dst = o + 8 * c;
+    if (((uintptr_t)dst & 15) == 0) {
+        *(u32x4 *)dst = u32x4{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
+                              (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16)};
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            dst[e] = h[e];
+    }
+}
+
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
 {
     constexpr int kBatch = 32;
@@ -375,6 +450,25 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
     const float ninf = -__builtin_inff();
     uint16_t *o = p.out + b * p.out_s_seq + qh * p.out_s_head;
 
+    // D = 128 (every MFMA decode) and at most 96 partials: four partials per
+    // load instruction, one round trip.
+    if (p.D == 128 && NS <= 96) {
+        if (NS <= 16)
+            merge_quads<4>(p, row0, rstep, NS, o);
+        else if (NS <= 24)
+            merge_quads<6>(p, row0, rstep, NS, o);
+        else if (NS <= 32)
+            merge_quads<8>(p, row0, rstep, NS, o);
+        else if (NS <= 48)
+            merge_quads<12>(p, row0, rstep, NS, o);
+        else if (NS <= 64)
+            merge_quads<16>(p, row0, rstep, NS, o);
+        else if (NS <= 80)
+            merge_quads<20>(p, row0, rstep, NS, o);
+        else
+            merge_quads<24>(p, row0, rstep, NS, o);
+        return;
+    }
     // At most 128 partials and D <= 128 (the usual case): one round trip,
     // every (m, l) and O row loaded together, the max taken over the batch.
     if (NS <= 32 && p.D <= 128) {
