@@ -136,17 +136,21 @@ def test_batched_ragged_split_invariance(dev, pps):
         _close(out[b], _oracle_batched(c, Hq, H, D, b), f"b={b} pps={pps}")
 
 
-@pytest.mark.parametrize("Hq,pps", [(8, 16), (8, 6), (8, 3), (8, 2), (16, 3)])
-def test_merge_partial_counts(dev, Hq, pps):
+@pytest.mark.parametrize("Hq,pps,pages", [(8, 16, 300), (8, 6, 300), (8, 3, 300), (8, 2, 300), (16, 3, 300),
+                                          (8, 20, 300), (8, 10, 300), (8, 8, 300), (8, 4, 300), (8, 4, 340),
+                                          (16, 5, 300)])
+def test_merge_partial_counts(dev, Hq, pps, pages):
     """One long sequence cut into many partials per (sequence, KV head): at
-    least pps units per wave gives about 20, 52, 103 and 154 partials per pair
-    for pps 16, 6, 3 and 2 (306 units: 300 pages and 6 FP16 units), which takes
-    the merge through its one-pass paths for 32, 64 and 128 partials and its
-    two-pass path, for GQA groups of 4 and 8."""
+    least pps units per wave over 300 pages and 6 FP16 units gives 16, 20, 32,
+    39, 52, 62, 78, 103 and 154 partials per pair for pps 20, 16, 10, 8, 6, 5,
+    4, 3 and 2, and 340 pages at pps 4 give 88.  That takes the merge through
+    every unrolled instance of its four-partials-per-load path (up to 16, 24,
+    32, 48, 64, 80 and 96 partials, with 16 and 32 exactly at a bound), its
+    float2 path for 128 and its two-pass path, for GQA groups of 4 and 8."""
     B, H, D, G, dk = 1, 2, 128, 128, 16
-    c = _batched_case(dev, 50 + pps, B, Hq, H, D, G, dk, [32 + 300 * 128 + 50])
+    c = _batched_case(dev, 50 + pps + pages, B, Hq, H, D, G, dk, [32 + pages * 128 + 50])
     out = _run_batched(dev, c, pps)
-    _close(out[0], _oracle_batched(c, Hq, H, D, 0), f"Hq={Hq} pps={pps}")
+    _close(out[0], _oracle_batched(c, Hq, H, D, 0), f"Hq={Hq} pps={pps} pages={pages}")
 
 
 @pytest.mark.parametrize("case", ["gqa16", "b70_uniform", "b70_ragged", "no_boost", "page_count_poison"])
