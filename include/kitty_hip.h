@@ -280,7 +280,9 @@ int kitty_paged_decode_noalloc(const kitty_decode_args *args, kitty_stream_t str
  * val_tokens (the caller did not spill it with kitty_quantize_kv_blocks), is
  * left unchanged and overflow[b] is set to 1.  Slots must be distinct within
  * one call.  Buffers and key / value rows must be 16-byte aligned, head_dim
- * a multiple of 8. */
+ * a multiple of 8, element strides multiples of 8, and the buffers' head
+ * strides non-negative with (H - 1) * s_head + head_dim < 2^30 (32-bit byte
+ * offsets inside a token's H x D block). */
 typedef struct {
     int64_t s_slot, s_head, s_tok; /* element strides; the channel stride is 1 */
 } kitty_slot_layout;
