@@ -21,7 +21,12 @@ events on the launch stream, right after `value` at the same settled clock
 upper bounds).
 
 `legs` repeats this for configs 4 and 5, each with its own roofline block;
-`quantize_pack` times config 2's batch quantize; `cpu_baseline` is the
+`quantize_pack` times config 2's batch quantize, `spill` the pipeline's spill
+launch, `module_forward` KittyPagedAttention.forward decode steps;
+`reference_items` runs the reference's own benchmark items (one-page key
+quantise / dequantise, push_token throughput, memory compression) with its
+defaults and timing method, and `widened_rows` times prefill (push_chunk) and
+the profiler's |K| accumulation at production shapes; `cpu_baseline` is the
 reference's CPU path restated op for op in torch (oracle/torch_reference.py)
 on every thread this process may use, `cpu_baseline_c_port` the scalar C
 restatement on one thread, both on a bounded sample of the config-3 step.
@@ -594,6 +599,169 @@ def decode_leg(torch, dev, name: str, copies: int, placement: str, steps: int, w
     return rec, (w if keep else None)
 
 
+def _host_median_ms(torch, fn, runs: int) -> float:
+    """Median wall-clock ms of fn() with a synchronisation before and after
+    every call (the reference benchmark's _timed_runs,
+    benchmark/benchmark_kitty_hardware.py:60-70)."""
+    times = []
+    for _ in range(runs):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(times)
+
+
+def _device_us(torch, fn, reps: int = 100) -> float:
+    """Mean µs per call of `reps` back-to-back calls between two HIP events
+    (median of five bursts): the device time without the host round trip."""
+    def burst() -> float:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+    return statistics.median(burst() for _ in range(5))
+
+
+def reference_items(torch, dev, runs: int = 100) -> dict:
+    """The reference's own benchmark (benchmark/benchmark_kitty_hardware.py)
+    on this build, with its defaults (32 layers, 8 KV heads, D = G = 128,
+    boost rate 0.125, 8,192-token sequences, :330-352) and its timing (each
+    call between two synchronisations, median of `runs`): one-page key
+    quantise (:110-147) and dequantise (:159-193) through the
+    reference-signature wrappers, push_token throughput for one sequence on
+    layer 0 with the same random tokens drawn per step (:200-241), and the
+    memory compression against an FP16 cache (:85-107).  Device-side time per
+    call (back-to-back calls between HIP events) is reported beside the host
+    figures, which are mostly launch and synchronisation latency."""
+    from kitty import KittyConfig, KittyInferencePipeline, PageCentricKVLayoutManager
+    from kitty.kernels.dequantize_key import dequantize_key_page
+    from kitty.kernels.quantize_key import quantize_key_page
+    cfg = KittyConfig(num_layers=32, num_kv_heads=8, head_dim=128, boost_rate=0.125, max_seq_len=8192,
+                      device=str(dev))
+    D, G, K, sent = cfg.head_dim, cfg.q_buffer_size, cfg.d_boost, cfg.sentinel
+    bi = torch.full((D,), sent, dtype=torch.uint8, device=dev)
+    bi[:K] = torch.arange(K, dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev).manual_seed(11)
+    key = torch.randn(D, G, dtype=torch.float16, device=dev, generator=g)
+    ob = torch.zeros(D, G // 4, dtype=torch.uint8, device=dev)
+    oh = torch.zeros(K, G // 4, dtype=torch.uint8, device=dev)
+    osc = torch.zeros(D, dtype=torch.float16, device=dev)
+    oz = torch.zeros(D, dtype=torch.float16, device=dev)
+    out16 = torch.zeros(D, G, dtype=torch.float16, device=dev)
+
+    def quant():
+        quantize_key_page(key, bi, K, sent, ob, oh, osc, oz)
+
+    def dequant():
+        dequantize_key_page(ob, oh, osc, oz, bi, K, out16)
+
+    res = {"config": "reference benchmark defaults: 32 layers, 8 KV heads, D = G = 128, boost 0.125, "
+                     "max_seq_len 8192", "runs": runs}
+    for name, fn, nbytes in (("quantize_key_page", quant, D * G * 2), ("dequantize_key_page", dequant, D * G * 2)):
+        for _ in range(5):
+            fn()
+        ms = _host_median_ms(torch, fn, runs)
+        res[name] = {"latency_ms": round(ms, 4), "bandwidth_GBps": round(nbytes / (ms * 1e-3) / 1e9, 3),
+                     "device_us": round(_device_us(torch, fn), 2)}
+
+    L, H, T = cfg.num_layers, cfg.num_kv_heads, cfg.max_seq_len
+    bidx = torch.full((L, H, D), sent, dtype=torch.uint8, device=dev)
+    bidx[:, :, :K] = torch.arange(K, dtype=torch.uint8, device=dev)
+    layout = PageCentricKVLayoutManager(cfg, bidx)
+    pipe = KittyInferencePipeline(cfg, layout, bidx)
+
+    def token():
+        k = torch.randn(H, D, dtype=torch.float16, device=dev, generator=g)
+        v = torch.randn(H, D, dtype=torch.float16, device=dev, generator=g)
+        pipe.push_token(layer_id=0, key=k, value=v, seq_id=0)
+
+    for _ in range(cfg.sink_size):
+        token()
+    steps = min(500, cfg.max_seq_len - cfg.sink_size - 1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        token()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    res["decode_throughput"] = {"num_steps": steps, "tokens_per_sec": round(steps / el, 1),
+                                "ms_per_token": round(el * 1e3 / steps, 4),
+                                "note": "push_token of one sequence, layer 0 (append, spills every G tokens)"}
+    mem = layout.memory_stats()
+    S, R = cfg.sink_size, cfg.local_value_window
+    fp16_bytes = L * 2 * H * T * D * 2
+    kitty = mem["total_MB"] * 1024 ** 2 + L * 2 * H * (S + G + R) * D * 2
+    res["memory_compression"] = {"fp16_cache_MB": round(fp16_bytes / 1024 ** 2, 1),
+                                 "kitty_total_MB": round(kitty / 1024 ** 2, 1),
+                                 "compression_ratio": round(fp16_bytes / kitty, 3)}
+    return res
+
+
+def widened_rows(torch, dev, B: int = 16, T: int = 4096, reps: int = 20) -> dict:
+    """The rows next to the decode path at production shapes: prefill (one
+    push_chunk of T prompt tokens for each of B sequences, one layer, 8 KV
+    heads x 128: sinks, (T - S) // G key pages quantised, FP16 buffers
+    written; pipeline.py push_chunk) and the profiler's |K| accumulation (one
+    kitty_channel_abs_sum launch over a (B, 8, T, 128) fp16 key tensor;
+    sensitivity.py:46-61), each as time per call and GB/s of fp16 input."""
+    from kitty import KittyConfig, KittyInferencePipeline, PageCentricKVLayoutManager
+    from kitty.sensitivity import _ChannelAccumulator
+    H, D = 8, 128
+    g = torch.Generator(device=dev).manual_seed(12)
+    keys = torch.randn(B, H, T, D, dtype=torch.float16, device=dev, generator=g)
+    values = torch.randn(B, H, T, D, dtype=torch.float16, device=dev, generator=g)
+    res = {"shape": f"B{B} x Hkv{H} x T{T} x D{D} fp16, one layer"}
+
+    import ctypes
+    from kitty import _hip
+    acc = _ChannelAccumulator(H, D, dev)
+    for _ in range(3):
+        acc.update(keys)
+    us_module = _device_us(torch, lambda: acc.update(keys), reps)
+    L = _hip.load()
+    need = ctypes.c_size_t(0)
+    _hip.check(L.kitty_channel_abs_sum_workspace_size(B, T, H, D, ctypes.byref(need)))
+    ws = torch.empty(max(need.value, 16), dtype=torch.uint8, device=dev)
+    sums = torch.zeros(H, D, dtype=torch.float32, device=dev)
+    args = (keys.data_ptr(), keys.stride(0), keys.stride(2), keys.stride(1), B, T, H, D, _hip.KITTY_DTYPE_F16,
+            sums.data_ptr(), ws.data_ptr(), need.value, _hip.stream_ptr(dev))
+    us = _device_us(torch, lambda: L.kitty_channel_abs_sum(*args), reps)
+    nbytes = keys.numel() * 2
+    res["profiler_abs_sum"] = {"us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1),
+                               "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4), "bytes_read": nbytes,
+                               "us_via_accumulator_update": round(us_module, 2),
+                               "note": "kitty_channel_abs_sum (two kernels) back to back with pre-built "
+                                       "arguments; the Python update() path beside it"}
+
+    cfg = KittyConfig(num_layers=1, num_kv_heads=H, head_dim=D, boost_rate=0.125, max_seq_len=T + 256,
+                      max_batch_size=B, device=str(dev))
+    bidx = torch.full((1, H, D), cfg.sentinel, dtype=torch.uint8, device=dev)
+    bidx[:, :, :cfg.d_boost] = torch.arange(cfg.d_boost, dtype=torch.uint8, device=dev)
+    layout = PageCentricKVLayoutManager(cfg, bidx)
+    pipe = KittyInferencePipeline(cfg, layout, bidx)
+    seqs = list(range(B))
+
+    def prefill():
+        for s in seqs:
+            pipe.reset_sequence(s)
+        pipe.push_chunk(0, keys, values, seqs)
+
+    for _ in range(2):
+        prefill()
+    ms = _host_median_ms(torch, prefill, reps)
+    nbytes = 2 * keys.numel() * 2
+    res["prefill_push_chunk"] = {"ms": round(ms, 3), "tokens_per_sec": round(B * T / (ms * 1e-3)),
+                                 "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                 "pages_per_seq": (T - cfg.sink_size) // cfg.q_buffer_size,
+                                 "note": "host clock around each call (resets of the B sequences included)"}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -613,6 +781,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-quantize", action="store_true")
     ap.add_argument("--no-module", action="store_true", help="skip the KittyPagedAttention.forward leg")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the reference benchmark's items and the prefill / profiler rows")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (HBM counter calibration)")
     args = ap.parse_args()
@@ -674,6 +844,11 @@ def main() -> int:
     if not args.no_module:
         log("timing KittyPagedAttention.forward decode steps")
         result["module_forward"] = module_leg(torch, dev, "cfg3")
+    if not args.no_extra:
+        log("timing the reference benchmark's items, prefill and the profiler accumulation")
+        result["reference_items"] = reference_items(torch, dev)
+        torch.cuda.empty_cache()
+        result["widened_rows"] = widened_rows(torch, dev)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define KITTY_ABI_VERSION 3
+#define KITTY_ABI_VERSION 4
 
 /* Element type of 16-bit data (the *_dtype fields below). */
 #define KITTY_DTYPE_F16 0
@@ -314,10 +314,19 @@ int kitty_append_tokens(const kitty_append_args *args, kitty_stream_t stream);
  * |key[b*s_b + t*s_t + h*s_h + d]| in fp32, key fp16 or bf16 (key_dtype,
  * the model's dtype) with a contiguous channel dimension (the hook's
  * (B, H, T, D) view of a key projection).  The summation order is fixed, so
- * repeated runs give identical sums. */
+ * repeated runs give identical sums.
+ * With a workspace of kitty_channel_abs_sum_workspace_size bytes (caller
+ * device memory, 16-byte aligned; the size depends on the shape only) and
+ * 16-byte rows (head_dim % 8 == 0 with 256 a multiple of head_dim / 8, key
+ * 16-byte aligned, strides multiples of 8 elements) the sums take two
+ * passes over chunks of tokens spread across the device; otherwise (NULL
+ * workspace or another shape) one workgroup per (head, 64 channels) sums
+ * every token. */
+int kitty_channel_abs_sum_workspace_size(int32_t batch, int32_t tokens, int32_t num_kv_heads, int32_t head_dim,
+                                         size_t *bytes);
 int kitty_channel_abs_sum(const uint16_t *key, int64_t s_b, int64_t s_t, int64_t s_h, int32_t batch,
                           int32_t tokens, int32_t num_kv_heads, int32_t head_dim, int32_t key_dtype, float *out,
-                          kitty_stream_t stream);
+                          void *workspace, size_t workspace_bytes, kitty_stream_t stream);
 
 #ifdef __cplusplus
 }

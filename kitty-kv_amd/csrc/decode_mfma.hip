@@ -725,7 +725,6 @@ __device__ __forceinline__ void page_segment(const DecodeParams &p, unsigned cha
 {
     constexpr int HPL = GQ / 4;
     constexpr int RSTEP = 4 / HPL;
-    constexpr int ROWS_PER_HEAD = 16 / GQ;
     // lane-derived offsets are rebuilt per segment (the asm hides the lane
     // id): kept across the caller's segment loop they would be spilled
     int lane = threadIdx.x;

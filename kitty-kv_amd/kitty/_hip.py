@@ -18,7 +18,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 # KITTY_HIP_LIBRARY selects another build of the same ABI (e.g. a tuning variant).
 LIB_PATH = os.environ.get("KITTY_HIP_LIBRARY") or os.path.join(_HERE, "libkitty_hip.so")
 
-KITTY_ABI_VERSION = 3
+KITTY_ABI_VERSION = 4
 KITTY_OK = 0
 KITTY_E_INVALID = -1
 KITTY_E_HIP = -2
@@ -121,6 +121,7 @@ EXPORTED_SYMBOLS = (
     "kitty_dequantize_key_page", "kitty_dequantize_value_page",
     "kitty_decode_workspace_size", "kitty_decode_path", "kitty_paged_decode", "kitty_paged_decode_splits",
     "kitty_paged_decode_merge", "kitty_paged_decode_noalloc", "kitty_append_tokens", "kitty_channel_abs_sum",
+    "kitty_channel_abs_sum_workspace_size",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -152,7 +153,9 @@ def load() -> ctypes.CDLL:
     L.kitty_paged_decode_merge.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_paged_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     L.kitty_append_tokens.argtypes = [ctypes.POINTER(AppendArgs), _vp]
-    L.kitty_channel_abs_sum.argtypes = [_vp, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp]
+    L.kitty_channel_abs_sum_workspace_size.argtypes = [_i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_size_t)]
+    L.kitty_channel_abs_sum.argtypes = [_vp, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
+                                        ctypes.c_size_t, _vp]
     if L.kitty_abi_version() != KITTY_ABI_VERSION:
         raise ImportError(f"libkitty_hip ABI {L.kitty_abi_version()} != {KITTY_ABI_VERSION}")
     _lib = L

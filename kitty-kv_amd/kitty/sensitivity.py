@@ -38,6 +38,7 @@ class _ChannelAccumulator:
         self.head_dim = head_dim
         self.sum_abs = torch.zeros(num_kv_heads, head_dim, dtype=torch.float32, device=device)
         self.token_count = 0
+        self._ws: Optional[torch.Tensor] = None  # chunk sums of the two-pass kernel, grown on demand
 
     @torch.no_grad()
     def update(self, key: torch.Tensor) -> None:
@@ -52,9 +53,15 @@ class _ChannelAccumulator:
             key = key.to(torch.float16)  # the kernel reads fp16 or bf16 (a model's dtype)
         if key.stride(3) != 1:
             key = key.contiguous()
-        _hip.check(_hip.load().kitty_channel_abs_sum(
+        L = _hip.load()
+        need = ctypes.c_size_t(0)
+        _hip.check(L.kitty_channel_abs_sum_workspace_size(B, T, H, D, ctypes.byref(need)))
+        if need.value and (self._ws is None or self._ws.numel() < need.value or self._ws.device != dev):
+            self._ws = torch.empty(need.value, dtype=torch.uint8, device=dev)
+        ws = self._ws.data_ptr() if need.value else None
+        _hip.check(L.kitty_channel_abs_sum(
             key.data_ptr(), key.stride(0), key.stride(2), key.stride(1), B, T, H, D, _hip.dtype_code(key, "key"),
-            self.sum_abs.data_ptr(), _hip.stream_ptr(dev)))
+            self.sum_abs.data_ptr(), ws, need.value, _hip.stream_ptr(dev)))
         self.token_count += B * T
 
     def scores(self) -> torch.Tensor:

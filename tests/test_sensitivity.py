@@ -126,3 +126,55 @@ def test_hooks_on_key_projections(dev):
         torch.testing.assert_close(prof.scores_[l], ref, rtol=1e-4, atol=1e-6)
     _, want = rank_channels(prof.scores_, cfg.d_boost, cfg.sentinel)
     assert torch.equal(prof.boost_idx_uint8, want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,T,H,D,how", [
+    (50, 3, 2, 128, "two-pass"),     # 16 rows per step wrap several batch rows at once
+    (2, 1000, 3, 64, "two-pass"),    # 8 lanes per row, 32 rows per step
+    (1, 300, 2, 256, "two-pass"),    # 32 lanes per row, 8 rows per step
+    (2, 100, 2, 48, "fallback"),     # 6 lanes per row do not tile 256 threads
+    (2, 100, 2, 128, "misaligned"),  # rows not 16-byte aligned
+    (3, 200, 2, 128, "no-workspace"),
+])
+def test_abs_sum_paths(dev, B, T, H, D, how):
+    """kitty_channel_abs_sum through each of its paths against float64, and
+    the same bits on a repeated call (fixed summation order)."""
+    import ctypes
+    from kitty import _hip
+    g = torch.Generator().manual_seed(B * T + D)
+    raw = (torch.randn(B, H, T + 1, D, generator=g) * 3).half()
+    key = raw[:, :, 1:] if how == "misaligned" else raw[:, :, :T]
+    kd = raw.to(dev)[:, :, 1:] if how == "misaligned" else raw.to(dev)[:, :, :T]
+    L = _hip.load()
+    need = ctypes.c_size_t(0)
+    _hip.check(L.kitty_channel_abs_sum_workspace_size(B, T, H, D, ctypes.byref(need)))
+    assert (need.value > 0) == (how in ("two-pass", "misaligned", "no-workspace"))
+    ws = torch.empty(max(need.value, 16), dtype=torch.uint8, device=dev)
+    outs = []
+    for _ in range(2):
+        out = torch.zeros(H, D, dtype=torch.float32, device=dev)
+        wp = None if how == "no-workspace" else ws.data_ptr()
+        _hip.check(L.kitty_channel_abs_sum(kd.data_ptr(), kd.stride(0), kd.stride(2), kd.stride(1), B, T, H, D,
+                                           _hip.KITTY_DTYPE_F16, out.data_ptr(), wp, need.value,
+                                           _hip.stream_ptr(torch.device(dev))))
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+    want = key.double().abs().sum(dim=(0, 2)).numpy()
+    np.testing.assert_allclose(outs[0].numpy(), want, rtol=1e-5)
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_abs_sum_workspace_rejects_small_buffers():
+    """A workspace below kitty_channel_abs_sum_workspace_size is refused
+    before any device work (the pointers are never dereferenced)."""
+    import ctypes
+    from kitty import _hip
+    L = _hip.load()
+    need = ctypes.c_size_t(0)
+    _hip.check(L.kitty_channel_abs_sum_workspace_size(4, 4096, 8, 128, ctypes.byref(need)))
+    assert need.value == 8 * 64 * 128 * 4           # 4 x 4096 tokens per head: 64 chunks of 256
+    fake = 1 << 20
+    rc = L.kitty_channel_abs_sum(fake, 8 * 4096 * 128, 128, 4096 * 128, 4, 4096, 8, 128, _hip.KITTY_DTYPE_F16,
+                                 fake, fake, need.value - 4, None)
+    assert rc == _hip.KITTY_E_INVALID and b"workspace too small" in L.kitty_last_error()
