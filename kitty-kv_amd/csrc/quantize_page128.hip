@@ -217,6 +217,24 @@ __device__ __forceinline__ int64_t dest_page(const QuantLaunch &L, int o, int i,
 
 // ------------------------------------------------------------------- keys
 // quantize_key.py:69-124: per channel over the 128 tokens.
+// Channel-major key blocks (token stride 1, the reference signature's (D, G)
+// key): the thread's tile comes as eight 16-byte loads of 8 tokens of one
+// channel each and is transposed in registers to token rows (one v_perm_b32
+// per output word: the same 16-bit half of two channels' words).
+__device__ __forceinline__ void load_tile_channel_major(const uint16_t *src, int64_t s_chan, u32x4 (&r)[8])
+{
+    u32x4 c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        c[j] = __builtin_nontemporal_load((const u32x4 *)(src + j * s_chan));
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            r[k][j] = __builtin_amdgcn_perm(c[2 * j + 1][k >> 1], c[2 * j][k >> 1], (k & 1) ? 0x07060302u : 0x05040100u);
+}
+
+template <bool CHAN_MAJOR>
 __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds)
 {
     const kitty_page_store &st = L.st;
@@ -226,7 +244,11 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
     const int Dk = st.d_boost;
 
     u32x4 r[8];
-    load_rows(qb.key + o * qb.key_s_outer + i * qb.key_s_inner + 8 * cg, qb.key_s_tok, 8 * tt, 128, cg, r);
+    if constexpr (CHAN_MAJOR)
+        load_tile_channel_major(qb.key + o * qb.key_s_outer + i * qb.key_s_inner + 8 * cg * qb.key_s_chan + 8 * tt,
+                                qb.key_s_chan, r);
+    else
+        load_rows(qb.key + o * qb.key_s_outer + i * qb.key_s_inner + 8 * cg, qb.key_s_tok, 8 * tt, 128, cg, r);
     // boost rank of channel tid (threads 128.. load a copy and ignore it)
     const int b = qb.boost_idx[o * qb.boost_s_outer + i * qb.boost_s_inner + (tid & 127)];
     bool ok;
@@ -434,8 +456,12 @@ __global__ __launch_bounds__(kThreads) void quantize_page128_kernel(QuantLaunch 
     const int n = blockIdx.x;
     const int o = n / L.qb.n_inner, i = n - o * L.qb.n_inner;
     if (blockIdx.y == 0) {
-        if (L.qb.key)
-            key_block(L, o, i, lds);
+        if (L.qb.key) {
+            if (L.qb.key_s_chan == 1)
+                key_block<false>(L, o, i, lds);
+            else
+                key_block<true>(L, o, i, lds);
+        }
     } else if (L.qb.value) {
         value_block(L, o, i, lds);
     }
@@ -451,8 +477,10 @@ bool page128_supported(const kitty_page_store &st, const kitty_quant_batch &qb)
     if (st.meta_dtype != KITTY_DTYPE_F16 || qb.src_dtype != KITTY_DTYPE_F16)
         return false;  // bf16 blocks or pools: the shape-generic kernel
     if (qb.key) {
-        if (qb.key_s_chan != 1 || !al16(qb.key) || !mul(qb.key_s_outer, 8) || !mul(qb.key_s_inner, 8) ||
-            !mul(qb.key_s_tok, 8))
+        // token-major rows (channel stride 1) or channel-major rows (token stride 1)
+        const bool rows = qb.key_s_chan == 1 && mul(qb.key_s_tok, 8);
+        const bool cols = qb.key_s_tok == 1 && qb.key_s_chan != 1 && mul(qb.key_s_chan, 8);
+        if (!(rows || cols) || !al16(qb.key) || !mul(qb.key_s_outer, 8) || !mul(qb.key_s_inner, 8))
             return false;
         if (st.key_low_s_row != 32 || !al16(st.key_low) || !mul(st.key_low_s_page, 16) ||
             !mul(st.key_low_s_head, 16))
