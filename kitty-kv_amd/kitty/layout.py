@@ -72,7 +72,7 @@ class PageCentricKVLayoutManager:
         self._freed: List[int] = []
         self._num_free = P
         self._page_table: Dict[Tuple[int, int, int], int] = {}
-        self._pages: Dict[int, Page] = {}
+        self._seq_keys: Dict[int, set] = {}  # seq_id -> its (layer, page number) entries of the page table
 
     # ------------------------------------------------------------ allocation
     def _pop_lowest_free(self) -> int:
@@ -92,11 +92,26 @@ class PageCentricKVLayoutManager:
                 "Increase config.max_pages or reduce max_seq_len/max_batch_size.")
         phys = self._pop_lowest_free()
         self._num_free -= 1
-        page = Page(physical_idx=phys, layer_id=layer_id, head_id=-1, seq_id=seq_id,
-                    start_token=page_number * self.config.q_buffer_size)
         self._page_table[(seq_id, layer_id, page_number)] = phys
-        self._pages[phys] = page
-        return page
+        self._seq_keys.setdefault(seq_id, set()).add((layer_id, page_number))
+        return Page(physical_idx=phys, layer_id=layer_id, head_id=-1, seq_id=seq_id,
+                    start_token=page_number * self.config.q_buffer_size)
+
+    def allocate_run(self, seq_id: int, layer_id: int, first_page: int, count: int) -> List[int]:
+        """Physical pages for page numbers first_page .. first_page + count - 1
+        of one (sequence, layer), each the lowest free page as count
+        allocate_page calls would give, all or nothing."""
+        if count > self._num_free:
+            raise RuntimeError(
+                "KV Cache page pool exhausted! "
+                f"{self._num_free} free pages, {count} needed.")
+        phys = [self._pop_lowest_free() for _ in range(count)]
+        self._num_free -= count
+        keys = self._seq_keys.setdefault(seq_id, set())
+        for j, ph in enumerate(phys):
+            self._page_table[(seq_id, layer_id, first_page + j)] = ph
+            keys.add((layer_id, first_page + j))
+        return phys
 
     def allocate_pages(self, seq_id: int, layer_ids: Sequence[int], page_number: int) -> List[int]:
         """Allocate one page per layer for a spill; all-or-nothing."""
@@ -110,13 +125,17 @@ class PageCentricKVLayoutManager:
         phys = self._page_table.pop((seq_id, layer_id, page_number), None)
         if phys is None:
             return
-        self._pages.pop(phys, None)
+        keys = self._seq_keys.get(seq_id)
+        if keys is not None:
+            keys.discard((layer_id, page_number))
         heapq.heappush(self._freed, phys)
         self._num_free += 1
 
     def free_sequence(self, seq_id: int) -> None:
-        for key in [k for k in self._page_table if k[0] == seq_id]:
-            self.free_page(*key)
+        for layer_id, page_number in sorted(self._seq_keys.pop(seq_id, ())):
+            phys = self._page_table.pop((seq_id, layer_id, page_number))
+            heapq.heappush(self._freed, phys)
+            self._num_free += 1
 
     def get_physical_idx(self, seq_id: int, layer_id: int, page_number: int) -> int:
         key = (seq_id, layer_id, page_number)

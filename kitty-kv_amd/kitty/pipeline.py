@@ -276,8 +276,8 @@ class KittyInferencePipeline:
                 count = 1 if counts is None else int(counts[i])
                 if first + count > self.max_pages_per_seq:
                     raise RuntimeError(f"sequence {seq} exceeds max_seq_len={self.config.max_seq_len}")
-                for j in range(count):
-                    taken.append((seq, first + j, self.layout.allocate_page(seq, layer, first + j).physical_idx))
+                for j, ph in enumerate(self.layout.allocate_run(seq, layer, first, count)):
+                    taken.append((seq, first + j, ph))
         except RuntimeError:
             for seq, pno, _ in taken:
                 self.layout.free_page(seq, layer, pno)
@@ -342,6 +342,11 @@ class KittyInferencePipeline:
         values = values.to(self.device, self._dtype)
         T = keys.shape[2]
         l = layer_id
+        slots = np.array([self.slot(seq) for seq in seq_ids], dtype=np.int64)
+        fresh = not any(c[slots, l].any() for c in (self._fill, self._qlen, self._npages, self._npv, self._vlen))
+        if fresh and self._store is not None and len(set(slots.tolist())) == len(slots):
+            self._push_chunk_fresh(l, keys, values, slots, seq_ids)
+            return
         for i, seq in enumerate(seq_ids):
             s = self.slot(seq)
             t = 0
@@ -397,6 +402,50 @@ class KittyInferencePipeline:
                 self._vlen[s, l] = vrem
             self.lens[:, l, s] = self._h2d(np.array([self._fill[s, l], self._qlen[s, l], self._npages[s, l],
                                                      self._npv[s, l], self._vlen[s, l]]))
+
+    def _push_chunk_fresh(self, l: int, keys: torch.Tensor, values: torch.Tensor, slots: np.ndarray,
+                          seq_ids: Sequence[int]) -> None:
+        """push_chunk for sequences that hold nothing yet at layer l (a new
+        prompt), batched over the sequences: the same state as the
+        per-sequence path, from one copy per buffer kind, one key-page and one
+        value-page quantise launch for all of them, and one counter write."""
+        cfg = self.config
+        S, G, R = cfg.sink_size, cfg.q_buffer_size, cfg.local_value_window
+        B, H, T, D = keys.shape
+        n_s = min(T, S)
+        m = T - n_s
+        n_full = m // G                                     # key pages of every sequence
+        v_full = n_full if R == 0 else max(0, (m - R) // G)  # of them, pages whose value half fills now
+        rem, vrem = m - n_full * G, m - v_full * G
+        phys = self._alloc_spill(l, slots, seq_ids, [n_full] * B) if n_full else []   # all or nothing
+        sl = self._slots_tensor(slots).long()
+        if n_s:
+            self._sink_k[sl, l, :, :n_s] = keys[:, :, :n_s]
+            self._sink_v[sl, l, :, :n_s] = values[:, :, :n_s]
+
+        def blocks(x: torch.Tensor, n: int) -> torch.Tensor:       # (B * n, H, G, D), page-major per sequence
+            return x[:, :, n_s:n_s + n * G].unflatten(2, (n, G)).transpose(1, 2).reshape(B * n, H, G, D)
+
+        if n_full:
+            pages = self._h2d(np.asarray(phys))                      # sequence-major: b * n_full + p
+            quantize_into_pools(self._store, blocks(keys, n_full), blocks(values, n_full) if R == 0 else None,
+                                self.boost_idx_uint8[l], pages, cfg.sentinel)
+            self._block_table[l, sl, :n_full] = pages.view(B, n_full)
+            self._pages[slots, l, :n_full] = np.asarray(phys).reshape(B, n_full)
+            if R and v_full:
+                pages_v = pages.view(B, n_full)[:, :v_full].reshape(-1)
+                quantize_into_pools(self._store, None, blocks(values, v_full), None, pages_v, cfg.sentinel)
+        if rem:
+            self._qbuf_k[sl, l, :, :rem] = keys[:, :, n_s + n_full * G:]
+        if vrem:
+            self._vbuf[sl, l, :, :vrem] = values[:, :, n_s + v_full * G:]
+        self._fill[slots, l] = n_s
+        self._qlen[slots, l] = rem
+        self._npages[slots, l] = n_full
+        self._npv[slots, l] = v_full
+        self._vlen[slots, l] = vrem
+        lens = np.stack([c[slots, l] for c in (self._fill, self._qlen, self._npages, self._npv, self._vlen)])
+        self.lens[:, l, sl] = self._h2d(lens)
 
     # ------------------------------------------------------------- query
     def get_attention_context(self, layer_id: int, seq_id: int = 0) -> dict:
