@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define KITTY_ABI_VERSION 4
+#define KITTY_ABI_VERSION 5
 
 /* Element type of 16-bit data (the *_dtype fields below). */
 #define KITTY_DTYPE_F16 0
@@ -93,6 +93,9 @@ typedef struct {
  * Block (o, i), o < n_outer, i < n_inner, quantises the G x D fp16 (or, with
  * src_dtype KITTY_DTYPE_BF16, bf16) block
  *   key[o*key_s_outer + i*key_s_inner + t*key_s_tok + d*key_s_chan]
+ * (with outer_per_seq = n > 0, ABI version 5: o*key_s_outer becomes
+ *  (o / n)*key_s_seq + (o % n)*key_s_outer, so the pages of a batch of
+ *  sequences are read in place from a (seq, head, token, channel) prompt)
  * per channel (INT4 when boost_idx[d] < sentinel, else INT2) and the value
  * block (same indexing with value_*) per token, and writes them to
  * page page_ids[o], head i of `store`.  Value rows t >= value_rows are
@@ -114,6 +117,8 @@ typedef struct {
     int32_t value_rows;
     int32_t sentinel; /* KittyConfig.sentinel = min(d_boost + 1, 255) */
     int32_t src_dtype; /* key / value blocks: KITTY_DTYPE_F16 or KITTY_DTYPE_BF16 (ABI version 3) */
+    int32_t outer_per_seq;          /* 0, or pages per sequence (ABI version 5) */
+    int64_t key_s_seq, value_s_seq; /* sequence strides when outer_per_seq > 0 */
 } kitty_quant_batch;
 
 int kitty_quantize_kv_blocks(const kitty_page_store *store, const kitty_quant_batch *batch,

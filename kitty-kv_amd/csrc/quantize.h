@@ -18,6 +18,16 @@ struct QuantLaunch {
     kitty_quant_batch qb;
 };
 
+// Offset of block row o in a source: o counts the pages of outer_per_seq-page
+// sequences (sequence stride s_seq) when outer_per_seq > 0, else pages.
+__device__ __forceinline__ int64_t outer_offset(const kitty_quant_batch &qb, int o, int64_t s_seq, int64_t s_outer)
+{
+    if (qb.outer_per_seq <= 0)
+        return (int64_t)o * s_outer;
+    const int q = o / qb.outer_per_seq;
+    return (int64_t)q * s_seq + (int64_t)(o - q * qb.outer_per_seq) * s_outer;
+}
+
 __device__ __forceinline__ float clampf(float v, float lo, float hi)
 {
     v = v < lo ? lo : v;

@@ -30,7 +30,7 @@ __device__ void quantize_key_block(const QuantLaunch &L, int o, int i, unsigned 
     float *red_mn = (float *)(hbytes + ((D * G4 + 15) & ~15)); // 256
     float *red_mx = red_mn + kQuantThreads;
 
-    const uint16_t *src = qb.key + o * qb.key_s_outer + i * qb.key_s_inner;
+    const uint16_t *src = qb.key + outer_offset(qb, o, qb.key_s_seq, qb.key_s_outer) + i * qb.key_s_inner;
     const uint8_t *bsrc = qb.boost_idx + o * qb.boost_s_outer + i * qb.boost_s_inner;
     const int32_t page = qb.page_ids[o];
 
@@ -119,7 +119,7 @@ __device__ void quantize_value_block(const QuantLaunch &L, int o, int i, unsigne
     float *red_mn = (float *)smem;
     float *red_mx = red_mn + kQuantThreads;
 
-    const uint16_t *src = qb.value + o * qb.value_s_outer + i * qb.value_s_inner;
+    const uint16_t *src = qb.value + outer_offset(qb, o, qb.value_s_seq, qb.value_s_outer) + i * qb.value_s_inner;
     const int32_t page = qb.page_ids[o];
 
     const int nsl = kQuantThreads / G;
@@ -272,6 +272,8 @@ extern "C" int kitty_quantize_kv_blocks(const kitty_page_store *store, const kit
         return fail(KITTY_E_INVALID, "key quantisation needs boost_idx and key pools");
     if (qb.value && (!store->value || !store->value_scale || !store->value_zero))
         return fail(KITTY_E_INVALID, "value quantisation needs value pools");
+    if (qb.outer_per_seq < 0)
+        return fail(KITTY_E_INVALID, "outer_per_seq must be >= 0");
     if (qb.value_rows < 0 || qb.value_rows > store->page_tokens)
         return fail(KITTY_E_INVALID, "value_rows must be in [0, page_tokens]");
     if (qb.src_dtype != KITTY_DTYPE_F16 && qb.src_dtype != KITTY_DTYPE_BF16)

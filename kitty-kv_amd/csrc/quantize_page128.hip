@@ -245,10 +245,10 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
 
     u32x4 r[8];
     if constexpr (CHAN_MAJOR)
-        load_tile_channel_major(qb.key + o * qb.key_s_outer + i * qb.key_s_inner + 8 * cg * qb.key_s_chan + 8 * tt,
+        load_tile_channel_major(qb.key + outer_offset(qb, o, qb.key_s_seq, qb.key_s_outer) + i * qb.key_s_inner + 8 * cg * qb.key_s_chan + 8 * tt,
                                 qb.key_s_chan, r);
     else
-        load_rows(qb.key + o * qb.key_s_outer + i * qb.key_s_inner + 8 * cg, qb.key_s_tok, 8 * tt, 128, cg, r);
+        load_rows(qb.key + outer_offset(qb, o, qb.key_s_seq, qb.key_s_outer) + i * qb.key_s_inner + 8 * cg, qb.key_s_tok, 8 * tt, 128, cg, r);
     // boost rank of channel tid (threads 128.. load a copy and ignore it)
     const int b = qb.boost_idx[o * qb.boost_s_outer + i * qb.boost_s_inner + (tid & 127)];
     bool ok;
@@ -372,7 +372,7 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
     const int cg = lane & 15, tt = wave * 4 + (lane >> 4);
 
     u32x4 r[8];
-    load_rows(qb.value + o * qb.value_s_outer + i * qb.value_s_inner + 8 * cg, qb.value_s_tok, 8 * tt,
+    load_rows(qb.value + outer_offset(qb, o, qb.value_s_seq, qb.value_s_outer) + i * qb.value_s_inner + 8 * cg, qb.value_s_tok, 8 * tt,
               qb.value_rows, cg, r);
     bool ok;
     const int64_t page = dest_page(L, o, i, ok);
@@ -480,7 +480,8 @@ bool page128_supported(const kitty_page_store &st, const kitty_quant_batch &qb)
         // token-major rows (channel stride 1) or channel-major rows (token stride 1)
         const bool rows = qb.key_s_chan == 1 && mul(qb.key_s_tok, 8);
         const bool cols = qb.key_s_tok == 1 && qb.key_s_chan != 1 && mul(qb.key_s_chan, 8);
-        if (!(rows || cols) || !al16(qb.key) || !mul(qb.key_s_outer, 8) || !mul(qb.key_s_inner, 8))
+        if (!(rows || cols) || !al16(qb.key) || !mul(qb.key_s_outer, 8) || !mul(qb.key_s_inner, 8) ||
+            !mul(qb.key_s_seq, 8))
             return false;
         if (st.key_low_s_row != 32 || !al16(st.key_low) || !mul(st.key_low_s_page, 16) ||
             !mul(st.key_low_s_head, 16))
@@ -493,7 +494,7 @@ bool page128_supported(const kitty_page_store &st, const kitty_quant_batch &qb)
     }
     if (qb.value) {
         if (qb.value_s_chan != 1 || !al16(qb.value) || !mul(qb.value_s_outer, 8) || !mul(qb.value_s_inner, 8) ||
-            !mul(qb.value_s_tok, 8))
+            !mul(qb.value_s_tok, 8) || !mul(qb.value_s_seq, 8))
             return false;
         if (st.value_s_row != 32 || !al16(st.value) || !mul(st.value_s_page, 16) || !mul(st.value_s_head, 16))
             return false;

@@ -18,7 +18,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 # KITTY_HIP_LIBRARY selects another build of the same ABI (e.g. a tuning variant).
 LIB_PATH = os.environ.get("KITTY_HIP_LIBRARY") or os.path.join(_HERE, "libkitty_hip.so")
 
-KITTY_ABI_VERSION = 4
+KITTY_ABI_VERSION = 5
 KITTY_OK = 0
 KITTY_E_INVALID = -1
 KITTY_E_HIP = -2
@@ -70,7 +70,7 @@ class QuantBatch(ctypes.Structure):
         ("value_s_chan", _i64),
         ("boost_idx", _vp), ("boost_s_outer", _i64), ("boost_s_inner", _i64),
         ("page_ids", _vp), ("n_outer", _i32), ("n_inner", _i32), ("value_rows", _i32), ("sentinel", _i32),
-        ("src_dtype", _i32),
+        ("src_dtype", _i32), ("outer_per_seq", _i32), ("key_s_seq", _i64), ("value_s_seq", _i64),
     ]
 
 

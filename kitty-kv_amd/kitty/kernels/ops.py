@@ -76,23 +76,35 @@ def _quant_batch(store: _hip.PageStore, key: Optional[torch.Tensor], value: Opti
     ref = key if key is not None else value
     _need(ref is not None, "nothing to quantise")
     dev = _hip.require_device(key, value, boost_idx, page_ids)
-    n_outer, n_inner, G, D = ref.shape
+    _need(ref.dim() in (4, 5), "key / value blocks must be (n_outer, H, G, D) or (n_seq, pages, H, G, D)")
+    per_seq = ref.shape[1] if ref.dim() == 5 else 0
+    n_outer = ref.shape[0] * per_seq if per_seq else ref.shape[0]
+    n_inner, G, D = ref.shape[-3:]
     _need(G == store.page_tokens and D == store.head_dim and n_inner == store.num_kv_heads,
           "block shape does not match the pools")
     _need(page_ids.dtype == torch.int32 and page_ids.numel() == n_outer, "page_ids must be int32 (n_outer,)")
     b = _hip.QuantBatch()
     b.src_dtype = _dtype16("key and value blocks", key, value)
+    b.outer_per_seq = per_seq
     if key is not None:
-        _need(tuple(key.shape) == (n_outer, n_inner, G, D), "key shape")
+        _need(key.shape == ref.shape, "key shape")
         b.key = key.data_ptr()
-        b.key_s_outer, b.key_s_inner, b.key_s_tok, b.key_s_chan = key.stride()
+        if per_seq:
+            b.key_s_seq, b.key_s_outer, b.key_s_inner, b.key_s_tok, b.key_s_chan = key.stride()
+        else:
+            b.key_s_outer, b.key_s_inner, b.key_s_tok, b.key_s_chan = key.stride()
     if value is not None:
-        _need(tuple(value.shape) == (n_outer, n_inner, G, D), "value shape")
+        _need(value.shape == ref.shape, "value shape")
         b.value = value.data_ptr()
-        b.value_s_outer, b.value_s_inner, b.value_s_tok, b.value_s_chan = value.stride()
+        if per_seq:
+            b.value_s_seq, b.value_s_outer, b.value_s_inner, b.value_s_tok, b.value_s_chan = value.stride()
+        else:
+            b.value_s_outer, b.value_s_inner, b.value_s_tok, b.value_s_chan = value.stride()
     if key is not None:
         _need(boost_idx is not None and boost_idx.dtype == torch.uint8 and boost_idx.shape[-1] == D
               and boost_idx.stride(-1) == 1, "boost_idx must be uint8 (..., D) with contiguous rows")
+        _need(tuple(boost_idx.shape[:-1]) in ((n_outer, n_inner), (n_inner,)),
+              "boost_idx must be (n_outer, H, D) or (H, D)")
         b.boost_idx = boost_idx.data_ptr()
         if boost_idx.dim() == 3:
             b.boost_s_outer, b.boost_s_inner = boost_idx.stride(0), boost_idx.stride(1)
@@ -110,9 +122,11 @@ def quantize_into_pools(store: _hip.PageStore, key: Optional[torch.Tensor], valu
                         value_rows: Optional[int] = None) -> None:
     """One launch over an (outer, inner=head) grid of fp16 or bf16 blocks.
 
-    key / value: (n_outer, n_inner, G, D) fp16 or bf16 views (any strides);
-    boost_idx: (n_outer, n_inner, D) or (n_inner, D) uint8; page_ids: (n_outer,)
-    int32 device tensor of destination pages.
+    key / value: (n_outer, n_inner, G, D) fp16 or bf16 views (any strides),
+    or (n_seq, n_per, n_inner, G, D) views whose n_seq * n_per blocks are
+    taken sequence-major (n_outer = n_seq * n_per; a prompt's pages read in
+    place); boost_idx: (n_outer, n_inner, D) or (n_inner, D) uint8;
+    page_ids: (n_outer,) int32 device tensor of destination pages.
     """
     b, dev = _quant_batch(store, key, value, boost_idx, page_ids, sentinel, value_rows)
     _hip.check(_hip.load().kitty_quantize_kv_blocks(ctypes.byref(store), ctypes.byref(b), _hip.stream_ptr(dev)))

@@ -27,6 +27,7 @@ from __future__ import annotations
 
 import heapq
 from dataclasses import dataclass
+from itertools import repeat
 from typing import Dict, Iterable, List, Optional, Sequence, Tuple
 
 import torch
@@ -105,12 +106,25 @@ class PageCentricKVLayoutManager:
             raise RuntimeError(
                 "KV Cache page pool exhausted! "
                 f"{self._num_free} free pages, {count} needed.")
-        phys = [self._pop_lowest_free() for _ in range(count)]
+        freed = self._freed
+        if len(freed) <= count:
+            # every freed index is below the high-water mark: the lowest
+            # `count` free pages are all of them, in order, then a fresh run
+            phys = sorted(freed)
+            freed.clear()
+            hw = self._high_water
+            self._high_water = hw + count - len(phys)
+            phys.extend(range(hw, self._high_water))
+        elif count <= 8:
+            phys = [heapq.heappop(freed) for _ in range(count)]
+        else:
+            freed.sort()            # a sorted list is still a min-heap: take its head
+            phys = freed[:count]
+            del freed[:count]
         self._num_free -= count
-        keys = self._seq_keys.setdefault(seq_id, set())
-        for j, ph in enumerate(phys):
-            self._page_table[(seq_id, layer_id, first_page + j)] = ph
-            keys.add((layer_id, first_page + j))
+        numbers = range(first_page, first_page + count)
+        self._page_table.update(zip(zip(repeat(seq_id), repeat(layer_id), numbers), phys))
+        self._seq_keys.setdefault(seq_id, set()).update(zip(repeat(layer_id), numbers))
         return phys
 
     def allocate_pages(self, seq_id: int, layer_ids: Sequence[int], page_number: int) -> List[int]:

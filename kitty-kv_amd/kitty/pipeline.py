@@ -83,11 +83,14 @@ class KittyInferencePipeline:
         self._qbuf_k = torch.zeros(n, L, H, G, D, dtype=dt, device=dev)
         self._vbuf = torch.zeros(n, L, H, self.value_capacity, D, dtype=dt, device=dev)
         # host mirrors of the counters, (slot, layer)
-        self._fill = np.zeros((n, L), np.int64)     # sink tokens written
-        self._qlen = np.zeros((n, L), np.int64)     # keys in the key buffer
-        self._npages = np.zeros((n, L), np.int64)   # key pages of (slot, layer)
-        self._npv = np.zeros((n, L), np.int64)      # pages whose value half is written
-        self._vlen = np.zeros((n, L), np.int64)     # values in the value buffer
+        # host copies of the five counters, one array (rows in the order of
+        # self.lens) so that a batch's counters are read in one indexing
+        self._counts = np.zeros((5, n, L), np.int64)
+        self._fill = self._counts[_FILL]        # sink tokens written
+        self._qlen = self._counts[_QLEN]        # keys in the key buffer
+        self._npages = self._counts[_NPAGES]    # key pages of (slot, layer)
+        self._npv = self._counts[_NPAGES_V]     # pages whose value half is written
+        self._vlen = self._counts[_VLEN]        # values in the value buffer
         # device counters (kind, layer, slot): a (layer, slot range) is a contiguous (B,) int32 view
         self.lens = torch.zeros(5, L, n, dtype=torch.int32, device=dev)
         self._overflow = torch.zeros(n, dtype=torch.int32, device=dev)
@@ -269,20 +272,20 @@ class KittyInferencePipeline:
         RuntimeError is raised."""
         if self._store is None:
             raise RuntimeError("kitty (MI355X build) quantises only on ROCm devices")
-        taken: List[Tuple[int, int, int]] = []
+        taken: List[Tuple[int, int, List[int]]] = []   # (seq, first page number, its run)
         try:
             for i, (s, seq) in enumerate(zip(np.asarray(slots).tolist(), seq_ids)):
                 first = int(self._npages[s, layer])
                 count = 1 if counts is None else int(counts[i])
                 if first + count > self.max_pages_per_seq:
                     raise RuntimeError(f"sequence {seq} exceeds max_seq_len={self.config.max_seq_len}")
-                for j, ph in enumerate(self.layout.allocate_run(seq, layer, first, count)):
-                    taken.append((seq, first + j, ph))
+                taken.append((seq, first, self.layout.allocate_run(seq, layer, first, count)))
         except RuntimeError:
-            for seq, pno, _ in taken:
-                self.layout.free_page(seq, layer, pno)
+            for seq, first, run in taken:
+                for j in range(len(run)):
+                    self.layout.free_page(seq, layer, first + j)
             raise
-        return [t[2] for t in taken]
+        return [ph for _, _, run in taken for ph in run]
 
     def _spill(self, layer: int, kslots: np.ndarray, phys: List[int], vslots: np.ndarray) -> None:
         """Key spill of kslots (their full key buffers into the new pages
@@ -308,7 +311,7 @@ class KittyInferencePipeline:
             self._npv[vslots, layer] += 1
             self._vlen[vslots, layer] -= G
         touched = np.union1d(kslots, vslots[:v]).astype(np.int64)
-        lens_new = np.stack([c[touched, layer] for c in (self._fill, self._qlen, self._npages, self._npv, self._vlen)])
+        lens_new = self._counts[:, touched, layer]
         nt = len(touched)
         meta = self._h2d(np.concatenate([kslots, pno, np.asarray(phys, np.int64), vslots[:v], vphys, touched,
                                          lens_new.ravel()]))
@@ -343,7 +346,7 @@ class KittyInferencePipeline:
         T = keys.shape[2]
         l = layer_id
         slots = np.array([self.slot(seq) for seq in seq_ids], dtype=np.int64)
-        fresh = not any(c[slots, l].any() for c in (self._fill, self._qlen, self._npages, self._npv, self._vlen))
+        fresh = not self._counts[:, slots, l].any()
         if fresh and self._store is not None and len(set(slots.tolist())) == len(slots):
             self._push_chunk_fresh(l, keys, values, slots, seq_ids)
             return
@@ -400,15 +403,15 @@ class KittyInferencePipeline:
                 vrem = nv + m - v_full * G
                 self._vbuf[s, l, :, :vrem] = vall[:, v_full * G:]
                 self._vlen[s, l] = vrem
-            self.lens[:, l, s] = self._h2d(np.array([self._fill[s, l], self._qlen[s, l], self._npages[s, l],
-                                                     self._npv[s, l], self._vlen[s, l]]))
+            self.lens[:, l, s] = self._h2d(self._counts[:, s, l])
 
     def _push_chunk_fresh(self, l: int, keys: torch.Tensor, values: torch.Tensor, slots: np.ndarray,
                           seq_ids: Sequence[int]) -> None:
         """push_chunk for sequences that hold nothing yet at layer l (a new
         prompt), batched over the sequences: the same state as the
         per-sequence path, from one copy per buffer kind, one key-page and one
-        value-page quantise launch for all of them, and one counter write."""
+        value-page quantise launch for all of them (reading the pages in place
+        from the prompt tensors), and one counter write."""
         cfg = self.config
         S, G, R = cfg.sink_size, cfg.q_buffer_size, cfg.local_value_window
         B, H, T, D = keys.shape
@@ -418,20 +421,24 @@ class KittyInferencePipeline:
         v_full = n_full if R == 0 else max(0, (m - R) // G)  # of them, pages whose value half fills now
         rem, vrem = m - n_full * G, m - v_full * G
         phys = self._alloc_spill(l, slots, seq_ids, [n_full] * B) if n_full else []   # all or nothing
-        sl = self._slots_tensor(slots).long()
+        # one ascending run of slots (the usual case) is written through a
+        # slice: plain strided copies instead of indexed scatters
+        run = bool((np.diff(slots) == 1).all())
+        sl = slice(int(slots[0]), int(slots[0]) + B) if run else self._slots_tensor(slots).long()
         if n_s:
             self._sink_k[sl, l, :, :n_s] = keys[:, :, :n_s]
             self._sink_v[sl, l, :, :n_s] = values[:, :, :n_s]
 
-        def blocks(x: torch.Tensor, n: int) -> torch.Tensor:       # (B * n, H, G, D), page-major per sequence
-            return x[:, :, n_s:n_s + n * G].unflatten(2, (n, G)).transpose(1, 2).reshape(B * n, H, G, D)
+        def blocks(x: torch.Tensor, n: int) -> torch.Tensor:       # (B, n, H, G, D) view of the prompt's pages
+            return x[:, :, n_s:n_s + n * G].unflatten(2, (n, G)).transpose(1, 2)
 
         if n_full:
-            pages = self._h2d(np.asarray(phys))                      # sequence-major: b * n_full + p
+            phys = np.asarray(phys, np.int32)
+            pages = self._h2d(phys)                                  # sequence-major: b * n_full + p
             quantize_into_pools(self._store, blocks(keys, n_full), blocks(values, n_full) if R == 0 else None,
                                 self.boost_idx_uint8[l], pages, cfg.sentinel)
             self._block_table[l, sl, :n_full] = pages.view(B, n_full)
-            self._pages[slots, l, :n_full] = np.asarray(phys).reshape(B, n_full)
+            self._pages[slots, l, :n_full] = phys.reshape(B, n_full)
             if R and v_full:
                 pages_v = pages.view(B, n_full)[:, :v_full].reshape(-1)
                 quantize_into_pools(self._store, None, blocks(values, v_full), None, pages_v, cfg.sentinel)
@@ -444,8 +451,7 @@ class KittyInferencePipeline:
         self._npages[slots, l] = n_full
         self._npv[slots, l] = v_full
         self._vlen[slots, l] = vrem
-        lens = np.stack([c[slots, l] for c in (self._fill, self._qlen, self._npages, self._npv, self._vlen)])
-        self.lens[:, l, sl] = self._h2d(lens)
+        self.lens[:, l, sl] = self._h2d(self._counts[:, slots, l])
 
     # ------------------------------------------------------------- query
     def get_attention_context(self, layer_id: int, seq_id: int = 0) -> dict:

@@ -40,6 +40,10 @@ def test_invalid_arguments_are_rejected_without_launch():
     st.head_dim, st.page_tokens, st.num_kv_heads = 130, 128, 1
     b = _hip.QuantBatch()
     assert L.kitty_quantize_kv_blocks(ctypes.byref(st), ctypes.byref(b), None) == _hip.KITTY_E_INVALID
+    st.head_dim = 128
+    b.n_outer, b.n_inner, b.page_ids, b.outer_per_seq = 1, 1, 16, -1   # the id pointer is never read here
+    assert L.kitty_quantize_kv_blocks(ctypes.byref(st), ctypes.byref(b), None) == _hip.KITTY_E_INVALID
+    assert b"outer_per_seq" in L.kitty_last_error()
     a = _hip.DecodeArgs()
     a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.page_tokens = 1, 6, 4, 128, 128
     assert L.kitty_paged_decode(ctypes.byref(a), None) == _hip.KITTY_E_INVALID

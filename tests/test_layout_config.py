@@ -59,6 +59,35 @@ def test_freed_slot_reused_first_fit():
     assert lay.allocate_page(1, 0, 2).physical_idx == 4
 
 
+def test_allocate_run_matches_page_by_page_first_fit():
+    """allocate_run(count) takes the pages count allocate_page calls would,
+    with the freed heap shorter than, as long as, and longer than the run
+    (short runs pop the heap, long ones sort it and take its head), and
+    records the same page table."""
+    import random
+    rng = random.Random(3)
+    cfg = _cfg()
+    a, b = _layout(cfg), _layout(cfg)
+    live = []
+    for step in range(200):
+        if live and rng.random() < 0.45:
+            for _ in range(rng.randint(1, 12)):
+                if live:
+                    seq, pno = live.pop(rng.randrange(len(live)))
+                    a.free_page(seq, 0, pno)
+                    b.free_page(seq, 0, pno)
+            continue
+        seq, count = step, rng.choice([1, 2, 3, 5, 9, 20])
+        if count > a.memory_stats()["pages_free"]:
+            continue
+        run = a.allocate_run(seq, 0, 0, count)
+        one = [b.allocate_page(seq, 0, j).physical_idx for j in range(count)]
+        assert run == one, step
+        live += [(seq, j) for j in range(count)]
+    assert a._page_table == b._page_table and a._seq_keys == b._seq_keys
+    assert a.memory_stats() == b.memory_stats()
+
+
 def test_pool_exhaustion_raises():
     cfg = _cfg()
     lay = _layout(cfg)

@@ -188,6 +188,44 @@ def test_value_rows_zero_padding(dev, rows):
         assert np.array_equal(vp[0, h], pk) and _eq16(vm[0, h, :, 0], sv) and _eq16(vm[0, h, :, 1], zv)
 
 
+@pytest.mark.parametrize("D,G,Dk,H,S,n", [(128, 128, 16, 8, 32, 3), (128, 128, 32, 2, 0, 2), (64, 32, 8, 3, 5, 4)])
+def test_pages_read_in_place_from_a_prompt(dev, D, G, Dk, H, S, n):
+    """(n_seq, pages, H, G, D) views of a (B, H, T, D) prompt, quantised in
+    place with the sequence stride (outer_per_seq): every page bit-exact
+    against the oracle on the same tokens, and pools identical to the launch
+    over the same blocks copied out page-major (128 x 128 kernel for the first
+    two shapes, the shape-generic kernel for the last)."""
+    from kitty.kernels.ops import quantize_into_pools
+    gen = torch.Generator().manual_seed(D + G + S + n)
+    B, sentinel = 3, Dk + 1
+    Tt = S + n * G + 7
+    K, chans = outlier_keys(gen, (B, Tt), H, D, max(Dk, 1), 8.0)
+    K = K.permute(0, 2, 1, 3).contiguous()                    # (B, H, T, D)
+    V = torch.randn(B, H, Tt, D, generator=gen).half()
+    bi = torch.full((H, D), sentinel, dtype=torch.uint8)
+    for h in range(H):
+        bi[h, torch.randperm(D, generator=gen)[:Dk]] = torch.arange(Dk, dtype=torch.uint8)
+    P = B * n + 4
+    page_ids = torch.randperm(P, generator=gen)[:B * n].to(torch.int32).to(dev)
+    Kd, Vd, bid = K.to(dev), V.to(dev), bi.to(dev)
+    view = lambda x: x[:, :, S:S + n * G].unflatten(2, (n, G)).transpose(1, 2)   # (B, n, H, G, D), no copy
+    pools, store = _pools(P, H, D, G, Dk, dev)
+    quantize_into_pools(store, view(Kd), view(Vd), bid, page_ids, sentinel)
+    pools2, store2 = _pools(P, H, D, G, Dk, dev)
+    flat = lambda x: view(x).reshape(B * n, H, G, D)          # the page-major copy
+    quantize_into_pools(store2, flat(Kd), flat(Vd), bid, page_ids, sentinel)
+    torch.cuda.synchronize()
+    for a, b in zip(pools, pools2):
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+    Kn, Vn, ids = K.numpy(), V.numpy(), page_ids.cpu().numpy()
+    for b in range(B):
+        for p in range(n):
+            t0 = S + p * G
+            for h in range(H):
+                _check_page(pools, int(ids[b * n + p]), h, Kn[b, h, t0:t0 + G].T.copy(), Vn[b, h, t0:t0 + G].copy(),
+                            bi[h].numpy(), Dk, sentinel)
+
+
 def test_reference_signatures(dev):
     """quantize_key_page / quantize_value_page / dequantize_* with the
     reference's arguments, outputs written into strided pool views."""
