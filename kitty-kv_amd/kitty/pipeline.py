@@ -63,6 +63,11 @@ from .kernels.ops import pool_store, quantize_into_pools
 _FILL, _QLEN, _NPAGES, _NPAGES_V, _VLEN = 0, 1, 2, 3, 4
 
 
+def _is_run(slots: np.ndarray) -> bool:
+    """True for a non-empty ascending run of consecutive slots."""
+    return len(slots) > 0 and bool((np.diff(slots) == 1).all())
+
+
 class KittyInferencePipeline:
     def __init__(self, config: KittyConfig, layout: PageCentricKVLayoutManager, boost_idx_uint8: torch.Tensor,
                  num_slots: Optional[int] = None) -> None:
@@ -320,17 +325,28 @@ class KittyInferencePipeline:
         vsl, vpages = meta[o:o + v].long(), meta[o + v:o + 2 * v]
         o += 2 * v
         tsl, lens_dev = meta[o:o + nt].long(), meta[o + nt:o + 6 * nt].view(5, nt)
+        # an ascending run of slots (sequences that advance in lockstep) is
+        # read through a slice view of the buffers, other sets by a gather
+        rows = lambda t, sl, idx: t[int(sl[0]):int(sl[0]) + len(sl)] if _is_run(sl) else t.index_select(0, idx)
         if k:
-            kblk = self._qbuf_k[:, layer].index_select(0, ksl)            # (n, H, G, D)
-            vblk = self._vbuf[:, layer].index_select(0, ksl)[:, :, :G] if both else None
+            kblk = rows(self._qbuf_k[:, layer], kslots, ksl)             # (n, H, G, D)
+            vblk = rows(self._vbuf[:, layer], kslots, ksl)[:, :, :G] if both else None
             quantize_into_pools(self._store, kblk, vblk, self.boost_idx_uint8[layer], kpages, self.config.sentinel)
             self._block_table[layer, ksl, kpn] = kpages
         if v:
             vb = self._vbuf[:, layer]                                     # (slots, H, R + G, D)
-            vblk = vb.index_select(0, vsl)                                # a copy: the shift below reuses rows
-            quantize_into_pools(self._store, None, vblk[:, :, :G], None, vpages, self.config.sentinel)
-            if R:
-                vb[vsl, :, :R] = vblk[:, :, G:G + R]                      # the R newest values move to the front
+            if _is_run(vslots[:v]):
+                a = int(vslots[0])
+                vblk = vb[a:a + v]
+                quantize_into_pools(self._store, None, vblk[:, :, :G], None, vpages, self.config.sentinel)
+                if R:   # the R newest values move to the front, after the launch above read the oldest G
+                    src = vblk[:, :, G:G + R]
+                    vblk[:, :, :R] = src if R <= G else src.clone()       # overlapping rows need a copy first
+            else:
+                vblk = vb.index_select(0, vsl)                            # a copy: the shift below reuses rows
+                quantize_into_pools(self._store, None, vblk[:, :, :G], None, vpages, self.config.sentinel)
+                if R:
+                    vb[vsl, :, :R] = vblk[:, :, G:G + R]                  # the R newest values move to the front
         self.lens[:, layer, tsl] = lens_dev
 
     # ------------------------------------------------------------ prefill
@@ -423,8 +439,7 @@ class KittyInferencePipeline:
         phys = self._alloc_spill(l, slots, seq_ids, [n_full] * B) if n_full else []   # all or nothing
         # one ascending run of slots (the usual case) is written through a
         # slice: plain strided copies instead of indexed scatters
-        run = bool((np.diff(slots) == 1).all())
-        sl = slice(int(slots[0]), int(slots[0]) + B) if run else self._slots_tensor(slots).long()
+        sl = slice(int(slots[0]), int(slots[0]) + B) if _is_run(slots) else self._slots_tensor(slots).long()
         if n_s:
             self._sink_k[sl, l, :, :n_s] = keys[:, :, :n_s]
             self._sink_v[sl, l, :, :n_s] = values[:, :, :n_s]

@@ -72,8 +72,17 @@ def test_reference_pipeline_state(dev):
     assert p.sink_fill == 0 and p.key_qbuf_len == 0 and lay.memory_stats()["pages_used"] == 0  # :101-113
 
 
-def test_spilled_pages_are_bit_exact(dev):
-    cfg = _cfg(num_layers=2, head_dim=128, q_buffer_size=128, sink_size=32, boost_rate=0.125, max_batch_size=3)
+@pytest.mark.parametrize("extra,R", [((2, 1, 0), None), ((2, 0, 1), None), ((2, 0, 1), 0), ((1, 2, 2), 64),
+                                     ((2, 0, 2), 64)])
+def test_spilled_pages_are_bit_exact(dev, extra, R):
+    """Pages of every spill bit-exact against the oracle.  Sequence i pushes
+    S + extra[i] G (+5 for the first) tokens: spills of slots 0 and 1
+    together (a run of slots, read through slice views), of slots 0 and 2
+    (a gather), with the value window off (keys and values spill together)
+    and at R = 64 (value spills of slots 1 and 2, and of 0 and 2)."""
+    kw = {} if R is None else {"local_value_window": R}
+    cfg = _cfg(num_layers=2, head_dim=128, q_buffer_size=128, sink_size=32, boost_rate=0.125, max_batch_size=3,
+               **kw)
     L, H, D, G, S = cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, cfg.q_buffer_size, cfg.sink_size
     gen = torch.Generator().manual_seed(1)
     bi = torch.stack([torch.stack([torch.full((D,), cfg.sentinel, dtype=torch.uint8) for _ in range(H)])
@@ -82,7 +91,7 @@ def test_spilled_pages_are_bit_exact(dev):
         for h in range(H):
             bi[l, h, torch.randperm(D, generator=gen)[:cfg.d_boost]] = torch.arange(cfg.d_boost, dtype=torch.uint8)
     p, lay, _ = _pipe(cfg, bi)
-    n_tok = {0: S + 2 * G + 5, 1: S + G, 2: S + 3}
+    n_tok = {s: S + e * G + (5 if s == 0 else 3 * (e == 0)) for s, e in enumerate(extra)}
     hist = {s: [] for s in n_tok}
     for t in range(max(n_tok.values())):
         ids = [s for s in n_tok if t < n_tok[s]]
