@@ -6,8 +6,11 @@
 // multiple of D / 8, 16-byte aligned rows):
 // * abs_sum_chunks_kernel: one 256-thread workgroup per (head, chunk of
 //   consecutive (b, t) tokens); D / 8 lanes cover one token row with a
-//   16-byte load each, 256 / (D / 8) rows per step, 16 loads per thread
-//   issued together per round; each lane sums its tokens in order, the row
+//   16-byte load each, 256 / (D / 8) rows per step, 8 loads per thread
+//   issued together per round (52 registers: eight waves per SIMD, so the
+//   256 chunks x 8 heads of a large batch are resident at once on 256 CUs,
+//   where 16 loads per round took 84 registers, five waves and a second
+//   partial round of workgroups); each lane sums its tokens in order, the row
 //   groups are added in order in LDS, and the chunk's D sums go to the
 //   workspace, laid out [head][channel][chunk];
 // * abs_sum_finish_kernel: one wave per (head, channel); lane l adds chunks
@@ -26,8 +29,8 @@ namespace kitty {
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSumThreads = 256;
-constexpr int kSumLoads = 16;      // 16-byte loads per thread per round
-constexpr int kMaxChunks = 2048;   // chunks per head at most (workspace bound)
+constexpr int kSumLoads = 8;       // 16-byte loads per thread per round
+constexpr int kMaxChunks = 256;    // chunks per head at most (workspace bound)
 
 struct AbsSumShape {
     int B, T, H, D;

@@ -133,6 +133,7 @@ def test_hooks_on_key_projections(dev):
     (50, 3, 2, 128, "two-pass"),     # 16 rows per step wrap several batch rows at once
     (2, 1000, 3, 64, "two-pass"),    # 8 lanes per row, 32 rows per step
     (1, 300, 2, 256, "two-pass"),    # 32 lanes per row, 8 rows per step
+    (3, 12000, 2, 128, "two-pass"),  # more tokens than 256 chunks of one round: two rounds per chunk
     (2, 100, 2, 48, "fallback"),     # 6 lanes per row do not tile 256 threads
     (2, 100, 2, 128, "misaligned"),  # rows not 16-byte aligned
     (3, 200, 2, 128, "no-workspace"),
@@ -173,7 +174,7 @@ def test_abs_sum_workspace_rejects_small_buffers():
     L = _hip.load()
     need = ctypes.c_size_t(0)
     _hip.check(L.kitty_channel_abs_sum_workspace_size(4, 4096, 8, 128, ctypes.byref(need)))
-    assert need.value == 8 * 64 * 128 * 4           # 4 x 4096 tokens per head: 64 chunks of 256
+    assert need.value == 8 * 128 * 128 * 4          # 4 x 4096 tokens per head: 128 chunks of 128
     fake = 1 << 20
     rc = L.kitty_channel_abs_sum(fake, 8 * 4096 * 128, 128, 4096 * 128, 4, 4096, 8, 128, _hip.KITTY_DTYPE_F16,
                                  fake, fake, need.value - 4, None)
