@@ -734,11 +734,22 @@ def widened_rows(torch, dev, B: int = 16, T: int = 4096, reps: int = 20) -> dict
             sums.data_ptr(), ws.data_ptr(), need.value, _hip.stream_ptr(dev))
     us = _device_us(torch, lambda: L.kitty_channel_abs_sum(*args), reps)
     nbytes = keys.numel() * 2
+    _hip.check(L.kitty_channel_abs_sum_deferred_size(H, D, ctypes.byref(need)))
+    slots = torch.zeros(need.value, dtype=torch.uint8, device=dev)
+    dargs = args[:10] + (slots.data_ptr(), need.value, args[12])
+    us_def = _device_us(torch, lambda: L.kitty_channel_abs_sum_deferred(*dargs), reps)
+    us_flush = _device_us(torch, lambda: L.kitty_channel_abs_sum_flush(slots.data_ptr(), H, D, sums.data_ptr(),
+                                                                       args[12]), reps)
     res["profiler_abs_sum"] = {"us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1),
                                "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4), "bytes_read": nbytes,
+                               "us_deferred_update": round(us_def, 2),
+                               "frac_deferred_update": round(nbytes / us_def / 1e3 / HBM_PEAK_GBPS, 4),
+                               "us_flush": round(us_flush, 2),
                                "us_via_accumulator_update": round(us_module, 2),
                                "note": "kitty_channel_abs_sum (two kernels) back to back with pre-built "
-                                       "arguments; the Python update() path beside it"}
+                                       "arguments; kitty_channel_abs_sum_deferred (first pass into per-chunk "
+                                       "slots, what _ChannelAccumulator.update runs) and the flush that "
+                                       "finishes it once per read; the Python update() path"}
 
     cfg = KittyConfig(num_layers=1, num_kv_heads=H, head_dim=D, boost_rate=0.125, max_seq_len=T + 256,
                       max_batch_size=B, device=str(dev))

@@ -333,6 +333,24 @@ int kitty_channel_abs_sum(const uint16_t *key, int64_t s_b, int64_t s_t, int64_t
                           int32_t tokens, int32_t num_kv_heads, int32_t head_dim, int32_t key_dtype, float *out,
                           void *workspace, size_t workspace_bytes, kitty_stream_t stream);
 
+/* The same accumulation with the second pass deferred (ABI version 5), for a
+ * calibration loop that reads the sums once after many batches
+ * (_ChannelAccumulator.update per batch, .scores at the end,
+ * kitty/sensitivity.py:46-67): kitty_channel_abs_sum_deferred adds each
+ * chunk's sums into a slot buffer of kitty_channel_abs_sum_deferred_size
+ * bytes (num_kv_heads x head_dim x 256 fp32 slots, 16-byte aligned, zero
+ * before the first call), one pass over the keys; kitty_channel_abs_sum_flush
+ * adds the slots into out and zeroes them.  Shapes without 16-byte rows (size
+ * 0), or a NULL slot buffer, add into out at once, and the flush then does
+ * nothing for them.  The summation order is fixed by the sequence of calls,
+ * so the same calls give identical sums. */
+int kitty_channel_abs_sum_deferred_size(int32_t num_kv_heads, int32_t head_dim, size_t *bytes);
+int kitty_channel_abs_sum_deferred(const uint16_t *key, int64_t s_b, int64_t s_t, int64_t s_h, int32_t batch,
+                                   int32_t tokens, int32_t num_kv_heads, int32_t head_dim, int32_t key_dtype,
+                                   float *out, void *slots, size_t slots_bytes, kitty_stream_t stream);
+int kitty_channel_abs_sum_flush(void *slots, int32_t num_kv_heads, int32_t head_dim, float *out,
+                                kitty_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

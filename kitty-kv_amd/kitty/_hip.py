@@ -121,7 +121,8 @@ EXPORTED_SYMBOLS = (
     "kitty_dequantize_key_page", "kitty_dequantize_value_page",
     "kitty_decode_workspace_size", "kitty_decode_path", "kitty_paged_decode", "kitty_paged_decode_splits",
     "kitty_paged_decode_merge", "kitty_paged_decode_noalloc", "kitty_append_tokens", "kitty_channel_abs_sum",
-    "kitty_channel_abs_sum_workspace_size",
+    "kitty_channel_abs_sum_workspace_size", "kitty_channel_abs_sum_deferred_size", "kitty_channel_abs_sum_deferred",
+    "kitty_channel_abs_sum_flush",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -156,6 +157,9 @@ def load() -> ctypes.CDLL:
     L.kitty_channel_abs_sum_workspace_size.argtypes = [_i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_size_t)]
     L.kitty_channel_abs_sum.argtypes = [_vp, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
                                         ctypes.c_size_t, _vp]
+    L.kitty_channel_abs_sum_deferred_size.argtypes = [_i32, _i32, ctypes.POINTER(ctypes.c_size_t)]
+    L.kitty_channel_abs_sum_deferred.argtypes = L.kitty_channel_abs_sum.argtypes
+    L.kitty_channel_abs_sum_flush.argtypes = [_vp, _i32, _i32, _vp, _vp]
     if L.kitty_abi_version() != KITTY_ABI_VERSION:
         raise ImportError(f"libkitty_hip ABI {L.kitty_abi_version()} != {KITTY_ABI_VERSION}")
     _lib = L

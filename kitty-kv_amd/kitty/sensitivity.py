@@ -36,9 +36,23 @@ class _ChannelAccumulator:
     def __init__(self, num_kv_heads: int, head_dim: int, device) -> None:
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
-        self.sum_abs = torch.zeros(num_kv_heads, head_dim, dtype=torch.float32, device=device)
+        self._sum_abs = torch.zeros(num_kv_heads, head_dim, dtype=torch.float32, device=device)
         self.token_count = 0
-        self._ws: Optional[torch.Tensor] = None  # chunk sums of the two-pass kernel, grown on demand
+        # per-chunk running sums of the deferred kernel (zero between flushes),
+        # added into _sum_abs when sum_abs is read: one pass over the keys per
+        # update, the finishing pass once per read
+        self._slots: Optional[torch.Tensor] = None
+        self._pending = False
+
+    @property
+    def sum_abs(self) -> torch.Tensor:
+        """Σ|k| per (head, channel) over every update so far (fp32 (H, D))."""
+        if self._pending:
+            _hip.check(_hip.load().kitty_channel_abs_sum_flush(
+                self._slots.data_ptr(), self.num_kv_heads, self.head_dim, self._sum_abs.data_ptr(),
+                _hip.stream_ptr(self._sum_abs.device)))
+            self._pending = False
+        return self._sum_abs
 
     @torch.no_grad()
     def update(self, key: torch.Tensor) -> None:
@@ -47,21 +61,24 @@ class _ChannelAccumulator:
         if (H, D) != (self.num_kv_heads, self.head_dim):
             raise ValueError(f"key shape {tuple(key.shape)} does not match ({self.num_kv_heads}, {self.head_dim})")
         dev = _hip.require_device(key)
-        if self.sum_abs.device != dev:
-            self.sum_abs = self.sum_abs.to(dev)
+        if self._sum_abs.device != dev:
+            self._sum_abs = self.sum_abs.to(dev)      # pending slots flushed on the old device first
+            self._slots = None
         if key.dtype not in (torch.float16, torch.bfloat16):
             key = key.to(torch.float16)  # the kernel reads fp16 or bf16 (a model's dtype)
         if key.stride(3) != 1:
             key = key.contiguous()
         L = _hip.load()
-        need = ctypes.c_size_t(0)
-        _hip.check(L.kitty_channel_abs_sum_workspace_size(B, T, H, D, ctypes.byref(need)))
-        if need.value and (self._ws is None or self._ws.numel() < need.value or self._ws.device != dev):
-            self._ws = torch.empty(need.value, dtype=torch.uint8, device=dev)
-        ws = self._ws.data_ptr() if need.value else None
-        _hip.check(L.kitty_channel_abs_sum(
+        if self._slots is None:
+            need = ctypes.c_size_t(0)
+            _hip.check(L.kitty_channel_abs_sum_deferred_size(H, D, ctypes.byref(need)))
+            self._slots = torch.zeros(max(need.value, 16), dtype=torch.uint8, device=dev)
+            self._slots_bytes = need.value
+        _hip.check(L.kitty_channel_abs_sum_deferred(
             key.data_ptr(), key.stride(0), key.stride(2), key.stride(1), B, T, H, D, _hip.dtype_code(key, "key"),
-            self.sum_abs.data_ptr(), ws, need.value, _hip.stream_ptr(dev)))
+            self._sum_abs.data_ptr(), self._slots.data_ptr() if self._slots_bytes else None, self._slots_bytes,
+            _hip.stream_ptr(dev)))
+        self._pending = self._slots_bytes > 0
         self.token_count += B * T
 
     def scores(self) -> torch.Tensor:

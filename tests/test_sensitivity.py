@@ -166,6 +166,51 @@ def test_abs_sum_paths(dev, B, T, H, D, how):
     assert torch.equal(outs[0], outs[1])
 
 
+@pytest.mark.gpu
+def test_deferred_abs_sum_matches_float64_and_repeats():
+    """kitty_channel_abs_sum_deferred over updates of different shapes (one
+    more than 256 chunks of one round, one misaligned by an element, which
+    adds into out at once), with a flush in the middle and at the end: the
+    float64 sum, the same bits on a second run of the same calls, zeroed
+    slots, and a flush with nothing pending adds nothing."""
+    import ctypes
+    from kitty import _hip
+    L = _hip.load()
+    H, D = 3, 128
+    need = ctypes.c_size_t(0)
+    _hip.check(L.kitty_channel_abs_sum_deferred_size(H, D, ctypes.byref(need)))
+    assert need.value == H * D * 256 * 4
+    g = torch.Generator().manual_seed(77)
+    shapes = ((2, 700, False), (5, 3, False), (3, 12000, False), (1, 300, True))
+    keys = [(torch.randn(B, H, T, D, generator=g) * 2).half() for B, T, _ in shapes]
+
+    def run():
+        slots = torch.zeros(need.value, dtype=torch.uint8, device="cuda")
+        out = torch.zeros(H, D, dtype=torch.float32, device="cuda")
+        held = []
+        for n, ((B, T, off), k) in enumerate(zip(shapes, keys)):
+            flat = torch.empty(k.numel() + 1, dtype=torch.float16, device="cuda")
+            flat[int(off):int(off) + k.numel()] = k.flatten().cuda()
+            key = flat[int(off):int(off) + k.numel()].view(B, H, T, D)      # off: 2 bytes from 16-byte alignment
+            held.append(flat)
+            _hip.check(L.kitty_channel_abs_sum_deferred(key.data_ptr(), key.stride(0), key.stride(2), key.stride(1),
+                                                        B, T, H, D, _hip.KITTY_DTYPE_F16, out.data_ptr(),
+                                                        slots.data_ptr(), need.value, None))
+            if n == 1:
+                _hip.check(L.kitty_channel_abs_sum_flush(slots.data_ptr(), H, D, out.data_ptr(), None))
+        _hip.check(L.kitty_channel_abs_sum_flush(slots.data_ptr(), H, D, out.data_ptr(), None))
+        first = out.clone()
+        _hip.check(L.kitty_channel_abs_sum_flush(slots.data_ptr(), H, D, out.data_ptr(), None))
+        torch.cuda.synchronize()
+        assert torch.equal(out, first) and slots.count_nonzero() == 0
+        return out.cpu()
+
+    a, b = run(), run()
+    ref = sum(k.double().abs().sum(dim=(0, 2)) for k in keys)
+    np.testing.assert_allclose(a.double().numpy(), ref.numpy(), rtol=1e-5)
+    assert torch.equal(a, b)
+
+
 def test_abs_sum_workspace_rejects_small_buffers():
     """A workspace below kitty_channel_abs_sum_workspace_size is refused
     before any device work (the pointers are never dereferenced)."""
@@ -179,3 +224,11 @@ def test_abs_sum_workspace_rejects_small_buffers():
     rc = L.kitty_channel_abs_sum(fake, 8 * 4096 * 128, 128, 4096 * 128, 4, 4096, 8, 128, _hip.KITTY_DTYPE_F16,
                                  fake, fake, need.value - 4, None)
     assert rc == _hip.KITTY_E_INVALID and b"workspace too small" in L.kitty_last_error()
+    _hip.check(L.kitty_channel_abs_sum_deferred_size(8, 128, ctypes.byref(need)))
+    assert need.value == 8 * 128 * 256 * 4                 # 256 slots per (head, channel), any batch
+    rc = L.kitty_channel_abs_sum_deferred(fake, 8 * 4096 * 128, 128, 4096 * 128, 4, 4096, 8, 128,
+                                          _hip.KITTY_DTYPE_F16, fake, fake, need.value - 4, None)
+    assert rc == _hip.KITTY_E_INVALID and b"slot buffer too small" in L.kitty_last_error()
+    _hip.check(L.kitty_channel_abs_sum_deferred_size(8, 48, ctypes.byref(need)))
+    assert need.value == 0                                 # no 16-byte rows: deferred calls add at once
+    assert L.kitty_channel_abs_sum_flush(None, 8, 48, None, None) == 0
