@@ -340,7 +340,7 @@ def bench_quantize(torch, dev, reps: int = 64, cpu: bool = False) -> dict:
     return out
 
 
-def module_leg(torch, dev, cfg_name: str = "cfg3", cycles: int = 2) -> dict:
+def module_leg(torch, dev, cfg_name: str = "cfg3", cycles: int = 2, event_cycles: int = 4) -> dict:
     """KittyPagedAttention.forward decode steps at a config's shape, the
     drop-in module path: per step one token of every sequence through the
     pipeline (append; key and value spills every G steps) and the fused
@@ -349,13 +349,14 @@ def module_leg(torch, dev, cfg_name: str = "cfg3", cycles: int = 2) -> dict:
     run G untimed steps (one spill cycle: the first launch of every kernel
     and the first pinned staging buffer are set-up costs), then `cycles` x G
     steps are timed back to back (host clock, events on the stream), so each
-    sequence spills its keys and values `cycles` times.  A last pass with an
-    event per step separates the spill steps."""
+    sequence spills its keys and values `cycles` times.  A last pass of
+    `event_cycles` x G steps with an event per step separates the spill steps
+    (the median over its cycles of each cycle's slowest step)."""
     from kitty import KittyConfig, KittyAttentionFactory
     c = CONFIGS[cfg_name]
     B, Hq, Hkv, ctx = c["B"], c["Hq"], c["Hkv"], c["ctx"]
     kcfg = KittyConfig(num_layers=1, num_kv_heads=Hkv, head_dim=D, q_buffer_size=G, sink_size=S,
-                       local_value_window=128, boost_rate=c["boost"], max_seq_len=ctx + (cycles + 2) * G,
+                       local_value_window=128, boost_rate=c["boost"], max_seq_len=ctx + (cycles + event_cycles + 1) * G,
                        max_batch_size=B, device=str(dev))
     gen = torch.Generator(device="cpu").manual_seed(c["seed"])
     dk = kcfg.d_boost
@@ -396,17 +397,19 @@ def module_leg(torch, dev, cfg_name: str = "cfg3", cycles: int = 2) -> dict:
     n_t = steps
     wall_us = (time.perf_counter() - t0) * 1e6 / n_t
     event_us = e0.elapsed_time(e1) * 1e3 / n_t
-    # per-step events over one more cycle of G steps: spill steps vs the rest
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(G + 1)]
+    # per-step events over event_cycles more cycles of G steps: spill steps vs the rest
+    n_ev = event_cycles * G
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev + 1)]
     torch.cuda.synchronize()
     ev[0].record()
-    for i in range(G):
+    for i in range(n_ev):
         attn(qs[i % steps], ks[i % steps], vs[i % steps], seq_id=seq_ids)
         ev[i + 1].record()
     torch.cuda.synchronize()
-    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(G)]
-    med = statistics.median(per)     # the sequences run in lockstep: one step of the G spills them all
-    worst = max(per)
+    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(n_ev)]
+    med = statistics.median(per)
+    # the sequences run in lockstep: one step of each cycle spills them all
+    worst = statistics.median(max(per[j * G:(j + 1) * G]) for j in range(event_cycles))
     plan = attn._plans.get(tuple(range(B)))
     assert plan is not None, "the decode plan is cached across steps"
     del layers, attn, pipe, layout, qs, ks, vs
@@ -416,7 +419,7 @@ def module_leg(torch, dev, cfg_name: str = "cfg3", cycles: int = 2) -> dict:
                         f"{int(c['boost'] * 1000) / 10}% INT4 keys",
             "us_per_step": round(wall_us, 2), "us_per_step_events": round(event_us, 2), "steps": n_t,
             "step_us_median": round(med, 2), "spill_step_us": round(worst, 2),
-            "spill_step_extra_us": round(worst - med, 2),
+            "spill_step_extra_us": round(worst - med, 2), "spill_steps_timed": event_cycles,
             "note": "each step: append of all B tokens, key/value spills every G steps (one key-only and one "
                     "value-only batch-quantize launch over B*Hkv blocks plus the value-buffer shift), decode "
                     "with independent key/value streams (page-pair split kernel, key-only pages in its FP16 "
