@@ -308,6 +308,61 @@ def test_bulk_prefill_matches_token_pushes(dev, D, G, S, pre, T, R):
     assert not a.overflowed() and not b.overflowed()
 
 
+def test_prefill_at_production_shape_is_bit_exact(dev):
+    """push_chunk of 4,096 tokens for 16 new sequences (the bench's prefill
+    shape: 8 KV heads x 128, 12.5 % INT4, S = 32, G = R = 128, outlier key
+    channels x8): the pages are read in place from the prompt; 24 sampled
+    (sequence, page) pairs, every head, bit-exact against the oracle (keys of
+    every page, values of the 30 pages older than the window), the FP16 sinks
+    and buffers equal to the prompt's rows, and the counters."""
+    from kitty import KittyConfig, KittyInferencePipeline, PageCentricKVLayoutManager
+    B, H, T, D, G, S, R = 16, 8, 4096, 128, 128, 32, 128
+    cfg = KittyConfig(num_layers=1, num_kv_heads=H, head_dim=D, boost_rate=0.125, max_seq_len=T + 256,
+                      max_batch_size=B, device="cuda:0")
+    assert (cfg.sink_size, cfg.q_buffer_size, cfg.local_value_window) == (S, G, R)
+    gen = torch.Generator().manual_seed(31)
+    K, chans = outlier_keys(gen, (B, T), H, D, cfg.d_boost, 8.0)         # (B, T, H, D)
+    calib, _ = outlier_keys(gen, (256,), H, D, cfg.d_boost, 8.0, channels=chans)
+    bi = calibrate_boost_idx(calib, cfg.d_boost, cfg.sentinel)           # (H, D)
+    Kd = K.permute(0, 2, 1, 3).contiguous().to(dev)                       # (B, H, T, D)
+    Vd = torch.randn(B, H, T, D, generator=gen).half().to(dev)
+    bid = bi[None].to(dev)
+    lay = PageCentricKVLayoutManager(cfg, bid)
+    pipe = KittyInferencePipeline(cfg, lay, bid)
+    pipe.push_chunk(0, Kd, Vd, list(range(B)))
+    torch.cuda.synchronize()
+    n_k, n_v = (T - S) // G, (T - S - R) // G                            # 31 key pages, 30 value pages
+    for c, want in (("_fill", S), ("_qlen", T - S - n_k * G), ("_npages", n_k), ("_npv", n_v),
+                    ("_vlen", T - S - n_v * G)):
+        assert (getattr(pipe, c)[:B, 0] == want).all(), c
+    assert torch.equal(pipe.lens[:, 0, :B].cpu(), torch.from_numpy(pipe._counts[:, :B, 0]).int())
+    Kc, Vc = Kd.cpu(), Vd.cpu()
+    for s in (0, 7, 15):
+        slot = pipe.slot(s)
+        assert torch.equal(pipe._sink_k[slot, 0, :, :S].cpu(), Kc[s, :, :S])
+        assert torch.equal(pipe._sink_v[slot, 0, :, :S].cpu(), Vc[s, :, :S])
+        q, v = T - S - n_k * G, T - S - n_v * G
+        assert torch.equal(pipe._qbuf_k[slot, 0, :, :q].cpu(), Kc[s, :, S + n_k * G:])
+        assert torch.equal(pipe._vbuf[slot, 0, :, :v].cpu(), Vc[s, :, S + n_v * G:])
+    kb, kh, km, vp, vm = (t.cpu().numpy() for t in (lay.key_baseline, lay.key_boost, lay.key_metadata,
+                                                     lay.value_pool, lay.value_metadata))
+    rng = np.random.default_rng(5)
+    picks = [(int(b), int(p)) for b, p in zip(rng.integers(0, B, 22), rng.integers(0, n_k, 22))]
+    picks += [(0, 0), (B - 1, n_k - 1)]
+    for s, p in picks:
+        ph = lay.get_page_list(s, 0)[p]
+        t0 = S + p * G
+        for h in range(H):
+            e = O.quantize_key(Kc[s, h, t0:t0 + G].T.numpy().copy(), bi[h].numpy(), cfg.d_boost, cfg.sentinel)
+            assert np.array_equal(kb[ph, h], e[0]) and np.array_equal(kh[ph, h], e[1]), (s, p, h)
+            assert np.array_equal(km[ph, h, 0].view(np.uint16), e[2].view(np.uint16)), (s, p, h)
+            assert np.array_equal(km[ph, h, 1].astype(np.float32), e[3].astype(np.float32)), (s, p, h)
+            if p < n_v:
+                ev = O.quantize_value(Vc[s, h, t0:t0 + G].numpy().copy())
+                assert np.array_equal(vp[ph, h], ev[0]), (s, p, h)
+                assert np.array_equal(vm[ph, h, :, 0].view(np.uint16), ev[1].view(np.uint16)), (s, p, h)
+
+
 def test_spill_on_full_pool_raises_and_leaves_state_unchanged(dev):
     """A push whose spill needs more pages than the pool has free raises the
     reference's exhaustion error (layout.py:161-203) before any state
