@@ -105,8 +105,12 @@ class KittyInferencePipeline:
         self._slot_of: Dict[int, int] = {}
         self._seq_of: Dict[int, int] = {}
         self._slots_dev: Dict[Tuple[int, ...], torch.Tensor] = {}
+        # append arguments per (layer, slots): everything but the token pointers
+        self._append_args: Dict[Tuple[int, Tuple[int, ...]], Tuple[_hip.AppendArgs, torch.Tensor]] = {}
         self._store = None
+        self._lib = None
         if dev.type == "cuda":
+            self._lib = _hip.load()
             self._store = pool_store(layout.key_baseline, layout.key_boost, layout.key_metadata,
                                      layout.value_pool, layout.value_metadata)
 
@@ -227,11 +231,25 @@ class KittyInferencePipeline:
         """kitty_append_tokens: every sequence's token into its buffers, one launch."""
         keys = keys if keys.stride(-1) == 1 else keys.contiguous()
         values = values if values.stride(-1) == 1 else values.contiguous()
-        sk, sv, qk, vb = (t[:, l] for t in (self._sink_k, self._sink_v, self._qbuf_k, self._vbuf))
-        a = _hip.AppendArgs()
+        ck = (l, tuple(slots.tolist()))
+        hit = self._append_args.get(ck)
+        if hit is None:
+            hit = self._append_args[ck] = self._append_setup(l, slots, keys.shape[1], keys.shape[2])
+            if len(self._append_args) > 256:
+                self._append_args.clear()
+                self._append_args[ck] = hit
+        a = hit[0]
         a.key, a.value = keys.data_ptr(), values.data_ptr()
         a.key_s_seq, a.key_s_head = keys.stride(0), keys.stride(1)
         a.value_s_seq, a.value_s_head = values.stride(0), values.stride(1)
+        _hip.check(self._lib.kitty_append_tokens(ctypes.byref(a), _hip.stream_ptr(self.device)))
+
+    def _append_setup(self, l: int, slots: np.ndarray, H: int, D: int) -> Tuple[_hip.AppendArgs, torch.Tensor]:
+        """kitty_append_tokens arguments of layer l for these slots, bar the
+        token pointers and strides (the buffers and counters never move), with
+        the slot-id tensor they point at."""
+        sk, sv, qk, vb = (t[:, l] for t in (self._sink_k, self._sink_v, self._qbuf_k, self._vbuf))
+        a = _hip.AppendArgs()
         slots_dev = self._slots_tensor(slots)
         a.slots = slots_dev.data_ptr()
         a.sink_k, a.sink_v = sk.data_ptr(), sv.data_ptr()
@@ -245,9 +263,9 @@ class KittyInferencePipeline:
         a.val_layout = _hip.SlotLayout(vb.stride(0), vb.stride(1), vb.stride(2))
         a.val_tokens = self.value_capacity
         a.overflow = self._overflow.data_ptr()
-        a.batch, a.num_kv_heads, a.head_dim = len(slots), keys.shape[1], keys.shape[2]
+        a.batch, a.num_kv_heads, a.head_dim = len(slots), H, D
         a.sink_size, a.buf_tokens, a.num_slots = self.config.sink_size, self.config.q_buffer_size, self.num_slots
-        _hip.check(_hip.load().kitty_append_tokens(ctypes.byref(a), _hip.stream_ptr(self.device)))
+        return a, slots_dev
 
     def _append_host(self, l: int, keys: torch.Tensor, values: torch.Tensor, slots: np.ndarray) -> None:
         """Buffer bookkeeping without a ROCm device (the FP16 buffers only;
