@@ -47,6 +47,8 @@ sys.path.insert(0, os.path.join(ROOT, "kitty-kv_amd"))
 HBM_PEAK_GBPS = 8000.0
 
 CONFIGS = {
+    # config 1: the reference's CPU-runnable case (one sequence, 8 Q / 8 KV heads, 1K context), here on the GPU
+    "cfg1": dict(B=1, Hq=8, Hkv=8, ctx=1024, boost=0.125, outlier=8.0, seed=1),
     "cfg3": dict(B=16, Hq=32, Hkv=8, ctx=32768, boost=0.125, outlier=8.0, seed=3),
     # config 4: ragged contexts drawn uniformly from [512, 65536] (seeded), 25 % INT4
     "cfg4": dict(B=64, Hq=32, Hkv=8, ctx=(512, 65536), boost=0.25, outlier=8.0, seed=4),
@@ -875,6 +877,7 @@ def main() -> int:
     if not args.no_module:
         log("timing KittyPagedAttention.forward decode steps")
         result["module_forward"] = module_leg(torch, dev, "cfg3")
+        result["module_forward_cfg1"] = module_leg(torch, dev, "cfg1")
     if not args.no_extra:
         log("timing the reference benchmark's items, prefill and the profiler accumulation")
         result["reference_items"] = reference_items(torch, dev)

@@ -155,6 +155,14 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
     p.meta_bf16 = a.meta_dtype == KITTY_DTYPE_BF16;
     p.act_bf16 = a.act_dtype == KITTY_DTYPE_BF16;
     p.sm_scale = a.sm_scale;
+    p.gq = p.GQ;
+    if (p.GQ == 1 || p.GQ == 2) {
+        // multi-head attention (and groups of 2) on the MFMA kernel of groups of 4
+        DecodeParams v = p;
+        v.GQ = 4;
+        if (mfma_path_supported(v))
+            p.GQ = 4;
+    }
     set_plan(p, a, mfma_path_supported(p));
     return KITTY_OK;
 }

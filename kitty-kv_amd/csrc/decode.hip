@@ -441,10 +441,10 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
     int NS = num_partials(p);
     int64_t row0 = (int64_t)bq * NS, rstep = 1;
     if (p.balanced) {
-        const int j = b * p.Hkv + qh / p.GQ;
+        const int j = b * p.Hkv + qh / p.gq;
         const int t0 = p.ws_pair[2 * j], t1 = p.ws_pair[2 * j + 1];
         NS = t1 - t0 + 1;
-        row0 = (int64_t)t0 * p.GQ + qh % p.GQ;
+        row0 = (int64_t)t0 * p.GQ + qh % p.gq;
         rstep = p.GQ;
     }
     const float ninf = -__builtin_inff();

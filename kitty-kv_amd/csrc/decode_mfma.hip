@@ -1,5 +1,6 @@
 // MFMA split-K paged decode for the production shape (D = G = 128,
-// D_boost <= 32, GQA group 4, 8 or 16) on gfx950.
+// D_boost <= 32, GQA group 4, 8 or 16; groups of 1 and 2 run as groups of 4
+// whose extra members repeat the first head) on gfx950.
 //
 // One wave (64 lanes) takes an equal share of the batch's work units (the
 // pages of every (sequence b, KV head kh) pair, then a weighted share of its
@@ -623,6 +624,13 @@ struct SegSetup {
     int ids;
 };
 
+// Query row of group member g of KV head kh (members past the real group,
+// gq < GQ, repeat its first head).
+__device__ __forceinline__ int64_t q_head(const DecodeParams &p, int kh, int g)
+{
+    return (int64_t)kh * p.gq + (g < p.gq ? g : 0);
+}
+
 template <int GQ>
 __device__ __forceinline__ SegSetup load_setup(const DecodeParams &p, int b, int kh, int p0, int p1)
 {
@@ -631,7 +639,7 @@ __device__ __forceinline__ SegSetup load_setup(const DecodeParams &p, int b, int
     SegSetup s;
     s.bi0 = p.boost_idx[kh * 128 + lane];
     s.bi1 = p.boost_idx[kh * 128 + 64 + lane];
-    const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + r / ROWS_PER_HEAD) * p.q_s_head;
+    const uint16_t *qrow = p.q + b * p.q_s_seq + q_head(p, kh, r / ROWS_PER_HEAD) * p.q_s_head;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         s.qraw[i] = *(const u32x4 *)(qrow + 32 * i + 8 * q);
@@ -686,7 +694,7 @@ __device__ __forceinline__ void qk_setup(WaveState<GQ> &W, const DecodeParams &p
         for (int i = 0; i < 8; ++i)
             W.hch[i] = rank_chan[8 * q + i];
         _Float16 qh[8];
-        const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + hr) * p.q_s_head;
+        const uint16_t *qrow = p.q + b * p.q_s_seq + q_head(p, kh, hr) * p.q_s_head;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             qh[i] = GQ <= 8 ? q_lds[hr * 128 + W.hch[i]] : *(const _Float16 *)(qrow + W.hch[i]);
@@ -986,7 +994,7 @@ __device__ void fp16_segments(const DecodeParams &p, int b, int kh, int lo, int 
     half8 qa[4];
     const float qk_c = p.sm_scale * kLog2e;
     {
-        const uint16_t *qrow = p.q + b * p.q_s_seq + (int64_t)(kh * GQ + (r < GQ ? r : 0)) * p.q_s_head;
+        const uint16_t *qrow = p.q + b * p.q_s_seq + q_head(p, kh, r < GQ ? r : 0) * p.q_s_head;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const u32x4 raw = *(const u32x4 *)(qrow + 32 * s + 8 * kq);

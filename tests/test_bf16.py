@@ -294,6 +294,9 @@ def test_decode_path_names_the_kernel(dev):
     def plan(b):
         return DecodePlan(q, bt, i32([3, 2]), *pools, b.to(dev), sk, sk, i32([S, S]), tk, tk, i32([5, 1]))
     assert plan(bi).kernel == "mfma"
+    q_mha = q[:, :H].contiguous()                      # one query head per KV head: padded to groups of 4
+    assert DecodePlan(q_mha, bt, i32([3, 2]), *pools, bi.to(dev), sk, sk, i32([S, S]), tk, tk,
+                      i32([5, 1])).kernel == "mfma"
     dup = bi.clone()
     dup[0, Dk] = 3                                   # rank 3 twice in head 0
     ops._warned_generic = False

@@ -33,7 +33,9 @@ def _to(dev, *arrs):
     (2, 8, 16, 8, 4, 2, 0, 3),
     (1, 4, 16, 8, 4, 0, 3, 0),      # sinks only (test_attention.py:190-215)
     (2, 4, 128, 128, 16, 5, 32, 96),
-    (8, 8, 128, 128, 16, 7, 32, 96),  # config 1 shape: ctx 1024 = 32 + 7*128 + 96
+    (8, 8, 128, 128, 16, 7, 32, 96),  # config 1 shape: ctx 1024 = 32 + 7*128 + 96 (MHA on the group-4 MFMA kernel)
+    (4, 8, 128, 128, 16, 9, 32, 50),  # groups of 2 on the group-4 MFMA kernel
+    (3, 3, 128, 128, 32, 20, 0, 128), # MHA, 25 % INT4, no sinks, a full tail
     (2, 16, 128, 128, 32, 3, 7, 0),
     (2, 4, 64, 32, 8, 6, 1, 31),
     (2, 4, 256, 128, 32, 2, 5, 17),   # generic kernel at the largest head_dim
