@@ -268,6 +268,7 @@ class DecodePlan:
         self.args = a
         self.out = out
         self.device = dev
+        self._sig = ((q.device, q.dtype, q.shape, q.stride()), (out.device, out.dtype, out.shape, out.stride()))
         # keep every tensor the kernels read alive as long as the plan
         self._keep = (q, block_table, num_pages, key_baseline, key_boost, key_meta, value_pool, value_meta,
                       boost_idx, sink_k, sink_v, sink_len, tail_k, tail_v, tail_len, workspace, num_pages_v,
@@ -281,9 +282,8 @@ class DecodePlan:
         """The same decode with another query and output of the plan's
         shapes and strides (a plan cached across decode steps: everything
         else it reads is device state that the steps update in place)."""
-        for name, t, ref in (("q", q, self._keep[0]), ("out", out, self.out)):
-            _need(t.device == self.device and t.dtype == ref.dtype and t.shape == ref.shape
-                  and t.stride() == ref.stride(), f"{name} must match the plan's dtype, shape, strides and device")
+        _need(((q.device, q.dtype, q.shape, q.stride()), (out.device, out.dtype, out.shape, out.stride())) == self._sig,
+              "q and out must match the plan's dtype, shape, strides and device")
         self.args.q, self.args.out = q.data_ptr(), out.data_ptr()
         try:
             _hip.check(self._L.kitty_paged_decode(ctypes.byref(self.args), _hip.stream_ptr(self.device)))

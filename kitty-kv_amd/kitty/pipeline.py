@@ -105,6 +105,8 @@ class KittyInferencePipeline:
         self._slot_of: Dict[int, int] = {}
         self._seq_of: Dict[int, int] = {}
         self._slots_dev: Dict[Tuple[int, ...], torch.Tensor] = {}
+        # slot arrays of batches of sequence ids seen before (cleared when a slot is freed)
+        self._slots_of_ids: Dict[Tuple[int, ...], np.ndarray] = {}
         # append arguments per (layer, slots): everything but the token pointers
         self._append_args: Dict[Tuple[int, Tuple[int, ...]], Tuple[_hip.AppendArgs, torch.Tensor]] = {}
         self._store = None
@@ -203,9 +205,15 @@ class KittyInferencePipeline:
         """One token for each of B sequences: keys / values (B, num_kv_heads, head_dim)."""
         cfg = self.config
         S, G = cfg.sink_size, cfg.q_buffer_size
-        slots = np.array([self.slot(s) for s in seq_ids], np.int64)
-        if len(set(slots.tolist())) != len(slots):
-            raise ValueError("a sequence appears twice in one push")
+        ids = tuple(seq_ids)
+        slots = self._slots_of_ids.get(ids)
+        if slots is None:
+            slots = np.array([self.slot(s) for s in ids], np.int64)
+            if len(set(slots.tolist())) != len(slots):
+                raise ValueError("a sequence appears twice in one push")
+            if len(self._slots_of_ids) >= 256:
+                self._slots_of_ids.clear()
+            self._slots_of_ids[ids] = slots
         keys = keys.to(self.device, self._dtype)
         values = values.to(self.device, self._dtype)
         l = layer_id
@@ -542,6 +550,7 @@ class KittyInferencePipeline:
         if s is None:
             return
         self._seq_of.pop(s, None)
+        self._slots_of_ids.clear()
         for c in (self._fill, self._qlen, self._npages, self._npv, self._vlen):
             c[s] = 0
         self._pages[s] = 0
