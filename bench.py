@@ -53,6 +53,8 @@ CONFIGS = {
     # config 4: ragged contexts drawn uniformly from [512, 65536] (seeded), 25 % INT4
     "cfg4": dict(B=64, Hq=32, Hkv=8, ctx=(512, 65536), boost=0.25, outlier=8.0, seed=4),
     "cfg5": dict(B=4, Hq=64, Hkv=8, ctx=131072, boost=0.125, outlier=16.0, seed=5),
+    # config 3's pages with one query head per KV head (multi-head attention, the padded MFMA group)
+    "mha": dict(B=16, Hq=8, Hkv=8, ctx=32768, boost=0.125, outlier=8.0, seed=3),
 }
 D, G, S = 128, 128, 32
 
