@@ -243,7 +243,7 @@ int kitty_paged_decode(const kitty_decode_args *args, kitty_stream_t stream);
 
 /* Which split kernel kitty_paged_decode runs for these arguments:
  * *path = KITTY_DECODE_PATH_MFMA (the production kernel: D = G = 128,
- * Dk <= 32, GQA 1 / 2 / 4 / 8 / 16 (1 and 2 padded to groups of 4), fp16,
+ * Dk <= 32, any GQA group up to 16 (padded to 4, 8 or 16), fp16,
  * 16-byte aligned buffers, unique boost
  * ranks) or KITTY_DECODE_PATH_GENERIC (every other shape the reference
  * accepts, about 15x slower at the production shape).  Mirrors the

@@ -156,12 +156,13 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
     p.act_bf16 = a.act_dtype == KITTY_DTYPE_BF16;
     p.sm_scale = a.sm_scale;
     p.gq = p.GQ;
-    if (p.GQ == 1 || p.GQ == 2) {
-        // multi-head attention (and groups of 2) on the MFMA kernel of groups of 4
+    if (p.GQ < 16 && p.GQ != 4 && p.GQ != 8) {
+        // other groups (multi-head attention, 2, 3, 6, 12, ...) on the MFMA
+        // kernel of the next group it builds, the extra members padding
         DecodeParams v = p;
-        v.GQ = 4;
+        v.GQ = p.GQ < 4 ? 4 : (p.GQ < 8 ? 8 : 16);
         if (mfma_path_supported(v))
-            p.GQ = 4;
+            p.GQ = v.GQ;
     }
     set_plan(p, a, mfma_path_supported(p));
     return KITTY_OK;

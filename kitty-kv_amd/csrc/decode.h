@@ -30,9 +30,9 @@ struct DecodeParams {
     const int32_t *tail_len_v;   // value tail tokens per sequence; NULL: tail_len
     int sink_cap, tail_cap, tail_v_cap;
     int B, Hq, Hkv, GQ, D, G, Dk;
-    // query heads per KV head.  GQ is the kernels' group: gq, or 4 for gq of
-    // 1 or 2 on the MFMA path, whose heads g >= gq repeat head 0 of the group
-    // and whose partial rows for them the merge never reads.
+    // query heads per KV head.  GQ is the kernels' group: gq, or on the MFMA
+    // path the next of 4, 8, 16 above it, whose members g >= gq repeat head 0
+    // of the group and whose partial rows for them the merge never reads.
     int gq;
     int max_pages, pages_per_split, n_splits;
     int n_fp16;   // FP16 splits per (b, kh) of the uniform plan (one)

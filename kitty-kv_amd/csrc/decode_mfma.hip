@@ -1,6 +1,6 @@
 // MFMA split-K paged decode for the production shape (D = G = 128,
-// D_boost <= 32, GQA group 4, 8 or 16; groups of 1 and 2 run as groups of 4
-// whose extra members repeat the first head) on gfx950.
+// D_boost <= 32, GQA group 4, 8 or 16; smaller groups run as the next of
+// these, whose extra members repeat the first head) on gfx950.
 //
 // One wave (64 lanes) takes an equal share of the batch's work units (the
 // pages of every (sequence b, KV head kh) pair, then a weighted share of its

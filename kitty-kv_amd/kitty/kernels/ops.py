@@ -258,7 +258,7 @@ class DecodePlan:
         path = ctypes.c_int32(0)
         _hip.check(self._L.kitty_decode_path(ctypes.byref(a), ctypes.byref(path)))
         self.kernel = "mfma" if path.value == _hip.KITTY_DECODE_PATH_MFMA else "generic"
-        if self.kernel == "generic" and D == 128 and G4 * 4 == 128 and Hq // Hkv in (4, 8, 16):
+        if self.kernel == "generic" and D == 128 and G4 * 4 == 128 and Hq // Hkv <= 16:
             _warn_generic(boost_unique, act_dtype, meta_dtype)
         need = ctypes.c_size_t(0)
         _hip.check(self._L.kitty_decode_workspace_size(ctypes.byref(a), ctypes.byref(need)))

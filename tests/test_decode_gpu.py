@@ -36,6 +36,9 @@ def _to(dev, *arrs):
     (8, 8, 128, 128, 16, 7, 32, 96),  # config 1 shape: ctx 1024 = 32 + 7*128 + 96 (MHA on the group-4 MFMA kernel)
     (4, 8, 128, 128, 16, 9, 32, 50),  # groups of 2 on the group-4 MFMA kernel
     (3, 3, 128, 128, 32, 20, 0, 128), # MHA, 25 % INT4, no sinks, a full tail
+    (2, 6, 128, 128, 16, 6, 32, 40),  # groups of 3 -> 4
+    (2, 12, 128, 128, 16, 5, 32, 7),  # groups of 6 -> 8
+    (1, 12, 128, 128, 16, 4, 32, 60), # a group of 12 -> 16
     (2, 16, 128, 128, 32, 3, 7, 0),
     (2, 4, 64, 32, 8, 6, 1, 31),
     (2, 4, 256, 128, 32, 2, 5, 17),   # generic kernel at the largest head_dim
