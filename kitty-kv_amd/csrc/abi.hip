@@ -161,8 +161,8 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
         // kernel of the next group it builds, the extra members padding
         DecodeParams v = p;
         v.GQ = p.GQ < 4 ? 4 : (p.GQ < 8 ? 8 : 16);
-        if (mfma_path_supported(v))
-            p.GQ = v.GQ;
+        if (mfma_path_supported(v) || (p.GQ != 1 && p.GQ != 2))
+            p.GQ = v.GQ;  // the generic kernel builds 1, 2, 4, 8 and 16 and pads the rest too
     }
     set_plan(p, a, mfma_path_supported(p));
     return KITTY_OK;

@@ -50,6 +50,13 @@ struct DecodeParams {
     int *ws_pair; // balanced: [B * Hkv][2] first and last partial t of each (b, kh)
 };
 
+// Query row of group member g of KV head kh (members past the real group,
+// gq < GQ, repeat its first head).
+__device__ __forceinline__ int64_t q_head(const DecodeParams &p, int kh, int g)
+{
+    return (int64_t)kh * p.gq + (g < p.gq ? g : 0);
+}
+
 // Stream lengths of sequence b, clamped to the buffer capacities.  The key
 // stream is sinks | npk key pages | nk key-tail tokens, the value stream
 // sinks | npv value pages | nv value-tail tokens; both cover the same tokens,

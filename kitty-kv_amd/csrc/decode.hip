@@ -183,7 +183,7 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
     const bool mbf = p.meta_bf16 != 0, abf = p.act_bf16 != 0;  // bf16 metadata / activations
     for (int e = tid; e < GQ * D; e += kGenThreads) {
         const int g = e / D, d = e - g * D;
-        s.qs[e] = x2f(p.q[b * p.q_s_seq + (int64_t)(kh * GQ + g) * p.q_s_head + d], abf) * qscale;
+        s.qs[e] = x2f(p.q[b * p.q_s_seq + q_head(p, kh, g) * p.q_s_head + d], abf) * qscale;
         s.O[e] = 0.0f;
     }
     if (tid < GQ) {
@@ -275,13 +275,13 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeParam
     }
     // ---------------------------------------------------- write partial
     const int NS = num_partials(p);
-    for (int e = tid; e < GQ * D; e += kGenThreads) {
+    for (int e = tid; e < p.gq * D; e += kGenThreads) {  // the real heads (gq <= GQ)
         const int g = e / D, d = e - g * D;
-        const int64_t row = ((int64_t)b * p.Hq + kh * GQ + g) * NS + split;
+        const int64_t row = ((int64_t)b * p.Hq + kh * p.gq + g) * NS + split;
         p.ws_o[row * D + d] = poison ? __builtin_nanf("") : s.O[e];
     }
-    if (tid < GQ) {
-        const int64_t row = ((int64_t)b * p.Hq + kh * GQ + tid) * NS + split;
+    if (tid < p.gq) {
+        const int64_t row = ((int64_t)b * p.Hq + kh * p.gq + tid) * NS + split;
         p.ws_ml[2 * row] = poison ? __builtin_nanf("") : s.m[tid];
         p.ws_ml[2 * row + 1] = s.l[tid];
     }
@@ -554,7 +554,7 @@ int launch_generic(const DecodeParams &p, hipStream_t stream)
     case 4: fn = (const void *)decode_generic_kernel<4>; break;
     case 8: fn = (const void *)decode_generic_kernel<8>; break;
     case 16: fn = (const void *)decode_generic_kernel<16>; break;
-    default: return fail(KITTY_E_UNSUPPORTED, "num_q_heads / num_kv_heads must be 1, 2, 4, 8 or 16");
+    default: return fail(KITTY_E_UNSUPPORTED, "num_q_heads / num_kv_heads must be at most 16");
     }
     if (lds > 64 * 1024 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
         return fail(KITTY_E_HIP, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");

@@ -624,13 +624,6 @@ struct SegSetup {
     int ids;
 };
 
-// Query row of group member g of KV head kh (members past the real group,
-// gq < GQ, repeat its first head).
-__device__ __forceinline__ int64_t q_head(const DecodeParams &p, int kh, int g)
-{
-    return (int64_t)kh * p.gq + (g < p.gq ? g : 0);
-}
-
 template <int GQ>
 __device__ __forceinline__ SegSetup load_setup(const DecodeParams &p, int b, int kh, int p0, int p1)
 {
