@@ -243,7 +243,9 @@ int kitty_paged_decode(const kitty_decode_args *args, kitty_stream_t stream);
 
 /* Which split kernel kitty_paged_decode runs for these arguments:
  * *path = KITTY_DECODE_PATH_MFMA (the production kernel: D = G = 128,
- * Dk <= 32, any GQA group up to 16 (padded to 4, 8 or 16), fp16,
+ * Dk <= 32, any GQA group (padded to 4, 8 or 16; groups above 16 run as
+ * sub-groups of 16 heads, one pass over the pages each, through
+ * kitty_paged_decode only), fp16,
  * 16-byte aligned buffers, unique boost
  * ranks) or KITTY_DECODE_PATH_GENERIC (every other shape the reference
  * accepts, about 15x slower at the production shape).  Mirrors the

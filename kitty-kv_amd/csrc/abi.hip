@@ -90,6 +90,8 @@ static void set_plan(DecodeParams &p, const kitty_decode_args &a, bool balanced)
     }
 }
 
+static void sub_group(DecodeParams &p, const kitty_decode_args &a, int s);
+
 static int build_params(const kitty_decode_args *args, DecodeParams &p)
 {
     if (!args)
@@ -144,9 +146,7 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
     p.tail_cap = a.tail_capacity > 0 ? a.tail_capacity : 0;
     p.tail_v_cap = a.tail_len_v ? (a.tail_v_capacity > 0 ? a.tail_v_capacity : 0) : p.tail_cap;
     p.B = a.batch;
-    p.Hq = a.num_q_heads;
     p.Hkv = a.num_kv_heads;
-    p.GQ = a.num_q_heads / a.num_kv_heads;
     p.D = a.head_dim;
     p.G = a.page_tokens;
     p.Dk = a.d_boost;
@@ -155,7 +155,21 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
     p.meta_bf16 = a.meta_dtype == KITTY_DTYPE_BF16;
     p.act_bf16 = a.act_dtype == KITTY_DTYPE_BF16;
     p.sm_scale = a.sm_scale;
-    p.gq = p.GQ;
+    p.gq_stride = a.num_q_heads / a.num_kv_heads;
+    p.sub_groups = (p.gq_stride + 15) / 16;
+    sub_group(p, a, 0);
+    return KITTY_OK;
+}
+
+// Sub-group s of the query heads (heads 16 s .. of every KV head's group):
+// its q / out pointers, group and kernel group, and the plan for them.
+static void sub_group(DecodeParams &p, const kitty_decode_args &a, int s)
+{
+    p.q = a.q ? a.q + (int64_t)16 * s * a.q_s_head : nullptr;
+    p.out = a.out ? a.out + (int64_t)16 * s * a.out_s_head : nullptr;
+    p.gq = std::min(16, p.gq_stride - 16 * s);
+    p.Hq = p.Hkv * p.gq;
+    p.GQ = p.gq;
     if (p.GQ < 16 && p.GQ != 4 && p.GQ != 8) {
         // other groups (multi-head attention, 2, 3, 6, 12, ...) on the MFMA
         // kernel of the next group it builds, the extra members padding
@@ -165,7 +179,6 @@ static int build_params(const kitty_decode_args *args, DecodeParams &p)
             p.GQ = v.GQ;  // the generic kernel builds 1, 2, 4, 8 and 16 and pads the rest too
     }
     set_plan(p, a, mfma_path_supported(p));
-    return KITTY_OK;
 }
 
 // Partial rows of the workspace: uniform plan B * Hq * (n_splits + 1);
@@ -186,6 +199,33 @@ static size_t workspace_bytes(const DecodeParams &p)
     return n;
 }
 
+// Workspace for every sub-group's plan (each sub-group's splits reuse the
+// memory of the one before; all but the last have sub-group 0's shape),
+// with kernel_alt also the plan of the other kernel at the MFMA shape (the
+// size must not depend on which kernel the real pointers select).
+static size_t workspace_need(const DecodeParams &p0, const kitty_decode_args &a, bool kernel_alt)
+{
+    size_t n = 0;
+    for (int s : {0, p0.sub_groups - 1}) {
+        DecodeParams q = p0;
+        sub_group(q, a, s);
+        n = std::max(n, workspace_bytes(q));
+        if (kernel_alt && mfma_shape_supported(q)) {
+            DecodeParams o = q;
+            set_plan(o, a, !q.balanced);
+            n = std::max(n, workspace_bytes(o));
+        }
+    }
+    return n;
+}
+
+static void set_workspace(DecodeParams &p, const kitty_decode_args &a)
+{
+    p.ws_o = (float *)a.workspace;
+    p.ws_ml = p.ws_o + workspace_rows(p) * p.D;
+    p.ws_pair = (int *)(p.ws_ml + workspace_rows(p) * 2);
+}
+
 } // namespace kitty
 
 using namespace kitty;
@@ -202,14 +242,7 @@ extern "C" int kitty_decode_workspace_size(const kitty_decode_args *args, size_t
         return rc;
     if (!bytes)
         return fail(KITTY_E_INVALID, "bytes is NULL");
-    // the size must not depend on which kernel the real pointers select
-    size_t n = workspace_bytes(p);
-    if (mfma_shape_supported(p)) {
-        DecodeParams o = p;
-        set_plan(o, *args, !p.balanced);
-        n = std::max(n, workspace_bytes(o));
-    }
-    *bytes = n;
+    *bytes = workspace_need(p, *args, true);
     return KITTY_OK;
 }
 
@@ -232,14 +265,19 @@ static int prepare(const kitty_decode_args *args, DecodeParams &p)
         return rc;
     if (!args->q || !args->out || !args->num_pages || !args->boost_idx || !args->sink_len || !args->tail_len)
         return fail(KITTY_E_INVALID, "NULL q, out, num_pages, boost_idx, sink_len or tail_len");
-    const size_t need = workspace_bytes(p);
+    const size_t need = workspace_need(p, *args, false);
     if (!args->workspace || args->workspace_bytes < need)
         return fail(KITTY_E_INVALID, "workspace too small: need " + std::to_string(need) + " bytes");
     if ((uintptr_t)args->workspace & 15)
         return fail(KITTY_E_INVALID, "workspace must be 16-byte aligned");
-    p.ws_o = (float *)args->workspace;
-    p.ws_ml = p.ws_o + workspace_rows(p) * p.D;
-    p.ws_pair = (int *)(p.ws_ml + workspace_rows(p) * 2);
+    set_workspace(p, *args);
+    return KITTY_OK;
+}
+
+static int one_group_only(const DecodeParams &p)
+{
+    if (p.sub_groups > 1)
+        return fail(KITTY_E_UNSUPPORTED, "groups above 16 query heads per KV head run through kitty_paged_decode");
     return KITTY_OK;
 }
 
@@ -247,7 +285,7 @@ extern "C" int kitty_paged_decode_splits(const kitty_decode_args *args, kitty_st
 {
     DecodeParams p;
     int rc = prepare(args, p);
-    if (rc || p.B == 0)
+    if (rc || p.B == 0 || (rc = one_group_only(p)))
         return rc;
     return launch_splits(p, (hipStream_t)stream);
 }
@@ -256,7 +294,7 @@ extern "C" int kitty_paged_decode_merge(const kitty_decode_args *args, kitty_str
 {
     DecodeParams p;
     int rc = prepare(args, p);
-    if (rc || p.B == 0)
+    if (rc || p.B == 0 || (rc = one_group_only(p)))
         return rc;
     return launch_merge(p, (hipStream_t)stream);
 }
@@ -267,10 +305,19 @@ extern "C" int kitty_paged_decode(const kitty_decode_args *args, kitty_stream_t 
     int rc = prepare(args, p);
     if (rc || p.B == 0)
         return rc;
-    rc = launch_splits(p, (hipStream_t)stream);
-    if (rc)
-        return rc;
-    return launch_merge(p, (hipStream_t)stream);
+    for (int s = 0; s < p.sub_groups; ++s) {
+        if (s > 0) {
+            sub_group(p, *args, s);
+            set_workspace(p, *args);
+        }
+        rc = launch_splits(p, (hipStream_t)stream);
+        if (rc)
+            return rc;
+        rc = launch_merge(p, (hipStream_t)stream);
+        if (rc)
+            return rc;
+    }
+    return KITTY_OK;
 }
 
 // ------------------------------------------------------------ no-alloc
@@ -311,7 +358,7 @@ extern "C" int kitty_paged_decode_noalloc(const kitty_decode_args *args, kitty_s
     int rc = build_params(args, p);
     if (rc || p.B == 0)
         return rc;
-    const size_t need = workspace_bytes(p);
+    const size_t need = workspace_need(p, *args, false);
     if (need > kScratchBytes)
         return fail(KITTY_E_INVALID, "kitty_paged_decode_noalloc: this batch needs " + std::to_string(need) +
                                          " bytes of scratch, the maximum is " + std::to_string(kScratchBytes) +

@@ -30,10 +30,14 @@ struct DecodeParams {
     const int32_t *tail_len_v;   // value tail tokens per sequence; NULL: tail_len
     int sink_cap, tail_cap, tail_v_cap;
     int B, Hq, Hkv, GQ, D, G, Dk;
-    // query heads per KV head.  GQ is the kernels' group: gq, or on the MFMA
-    // path the next of 4, 8, 16 above it, whose members g >= gq repeat head 0
+    // query heads per KV head of this launch.  GQ is the kernels' group: gq,
+    // or the next of 4, 8, 16 above it, whose members g >= gq repeat head 0
     // of the group and whose partial rows for them the merge never reads.
-    int gq;
+    // Groups above 16 run as sub-groups of at most 16 heads, one split +
+    // merge each: gq_stride is the whole group (the heads of KV head kh are
+    // rows kh * gq_stride .. of q and out), sub_groups their count; q and
+    // out then point at the sub-group's first head.
+    int gq, gq_stride, sub_groups;
     int max_pages, pages_per_split, n_splits;
     int n_fp16;   // FP16 splits per (b, kh) of the uniform plan (one)
     int flags;
@@ -54,7 +58,7 @@ struct DecodeParams {
 // gq < GQ, repeat its first head).
 __device__ __forceinline__ int64_t q_head(const DecodeParams &p, int kh, int g)
 {
-    return (int64_t)kh * p.gq + (g < p.gq ? g : 0);
+    return (int64_t)kh * p.gq_stride + (g < p.gq ? g : 0);
 }
 
 // Stream lengths of sequence b, clamped to the buffer capacities.  The key

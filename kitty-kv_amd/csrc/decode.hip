@@ -448,7 +448,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p)
         rstep = p.GQ;
     }
     const float ninf = -__builtin_inff();
-    uint16_t *o = p.out + b * p.out_s_seq + qh * p.out_s_head;
+    uint16_t *o = p.out + b * p.out_s_seq + ((int64_t)(qh / p.gq) * p.gq_stride + qh % p.gq) * p.out_s_head;
 
     // D = 128 (every MFMA decode) and at most 96 partials: four partials per
     // load instruction, one round trip.

@@ -126,3 +126,28 @@ def test_noalloc_rejects_batches_beyond_its_scratch():
     a.block_table = a.key_low = a.key_high = a.key_meta = a.value = a.value_meta = 1  # never dereferenced
     assert L.kitty_paged_decode_noalloc(ctypes.byref(a), None) == _hip.KITTY_E_INVALID
     assert b"maximum is 67108864" in L.kitty_last_error()
+
+
+def test_groups_above_16_run_only_through_the_whole_decode():
+    """A group of 40 query heads per KV head runs as sub-groups of 16, 16 and
+    8 through kitty_paged_decode; the split-only and merge-only entry points
+    refuse it before any launch, and the workspace covers the largest
+    sub-group's plan."""
+    from kitty import _hip
+    L = _hip.load()
+    a = _hip.DecodeArgs()
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.page_tokens, a.d_boost = 2, 40, 1, 128, 128, 16
+    a.max_pages, a.bt_stride = 8, 8
+    a.block_table = a.key_low = a.key_high = a.key_meta = a.value = a.value_meta = 16   # never dereferenced
+    need40 = ctypes.c_size_t(0)
+    _hip.check(L.kitty_decode_workspace_size(ctypes.byref(a), ctypes.byref(need40)))
+    a.num_q_heads = 16
+    need16 = ctypes.c_size_t(0)
+    _hip.check(L.kitty_decode_workspace_size(ctypes.byref(a), ctypes.byref(need16)))
+    assert need40.value == need16.value > 0
+    a.num_q_heads = 40
+    a.q = a.out = a.num_pages = a.boost_idx = a.sink_len = a.tail_len = 16
+    a.workspace, a.workspace_bytes = 256, need40.value
+    for fn in (L.kitty_paged_decode_splits, L.kitty_paged_decode_merge):
+        assert fn(ctypes.byref(a), None) == _hip.KITTY_E_UNSUPPORTED
+        assert b"groups above 16" in L.kitty_last_error()

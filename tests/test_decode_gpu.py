@@ -41,6 +41,9 @@ def _to(dev, *arrs):
     (1, 12, 128, 128, 16, 4, 32, 60), # a group of 12 -> 16
     (2, 6, 64, 32, 8, 5, 3, 9),       # generic kernel, groups of 3 -> 4
     (1, 12, 16, 8, 4, 6, 4, 5),       # generic kernel, a group of 12 -> 16
+    (1, 32, 128, 128, 16, 5, 32, 40), # multi-query attention: two sub-groups of 16
+    (2, 40, 128, 128, 16, 4, 32, 9),  # groups of 20: sub-groups of 16 and 4
+    (1, 24, 64, 32, 8, 5, 3, 9),      # generic kernel, a group of 24: 16 and 8
     (2, 16, 128, 128, 32, 3, 7, 0),
     (2, 4, 64, 32, 8, 6, 1, 31),
     (2, 4, 256, 128, 32, 2, 5, 17),   # generic kernel at the largest head_dim
