@@ -286,6 +286,35 @@ def quantize_cpu_baseline(k, v, bi, dk: int) -> dict:
                       f"single thread"}
 
 
+def quantize_cpu_baseline_torch(k, v, bi, dk: int) -> dict:
+    """The reference's quantize_key_page_torch / quantize_value_page_torch,
+    restated op for op in torch (oracle/torch_reference.py), over every block
+    of one config-2 batch with every thread torch may use here (the
+    reference's key loop takes each (D, G) block, its value loop each (G, D)
+    block, one call per (page, head))."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import torch
+    import torch_reference as TR
+    threads = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        kc, vc, bic = k.cpu(), v.cpu(), bi.cpu()                        # (T, H, D), (H, D)
+        T, H, _ = kc.shape
+        t0 = time.perf_counter()
+        for p0 in range(0, T, G):
+            for h in range(H):
+                TR.quantize_key_page(kc[p0:p0 + G, h].T.contiguous(), bic[h], dk, dk + 1)   # pipeline.py:219
+                TR.quantize_value_page(vc[p0:p0 + G, h])
+        us = (time.perf_counter() - t0) * 1e6
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": round(us, 1), "unit": "us/batch", "cores": threads, "kind": "port", **host_cpu(),
+            "sample": f"all {T // G * H} key + {T // G * H} value blocks of one config-2 batch through "
+                      f"oracle/torch_reference.py (quantize_key_page_torch / quantize_value_page_torch restated "
+                      f"op for op in torch, CPU, {threads} threads)"}
+
+
 def bench_quantize(torch, dev, reps: int = 64, cpu: bool = False) -> dict:
     """4096 tokens x 8 KV heads x 128, batch quantize + pack.
     Sixteen input / output sets (309 MB, more than the 256 MB MALL) rotate;
@@ -332,7 +361,8 @@ def bench_quantize(torch, dev, reps: int = 64, cpu: bool = False) -> dict:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps * 1e3
     us = statistics.median(burst() for _ in range(5))
-    cpu_base = quantize_cpu_baseline(k0, v0, bi, dk) if cpu else None
+    cpu_base = quantize_cpu_baseline_torch(k0, v0, bi, dk) if cpu else None
+    cpu_port = quantize_cpu_baseline(k0, v0, bi, dk) if cpu else None
     read = 2 * T * H * D * 2
     written = n * H * (D * G // 4 + dk * G // 4 + 2 * D * 2 + G * D // 4 + G * 2 * 2)
     out = {"workload": "cfg2: 4096 tok x 8 KV heads x 128, 16 x8 outlier key channels per head as INT4",
@@ -341,6 +371,7 @@ def bench_quantize(torch, dev, reps: int = 64, cpu: bool = False) -> dict:
            "bytes_read": read, "bytes_written": written}
     if cpu_base:
         out["cpu_baseline"] = cpu_base
+        out["cpu_baseline_c_port"] = cpu_port
     return out
 
 

@@ -1,4 +1,5 @@
-"""Op-for-op torch (CPU) restatement of the reference's paged decode path.
+"""Op-for-op torch (CPU) restatement of the reference's paged decode path
+and of its page quantisers.
 
 TEST INFRASTRUCTURE ONLY: timed as the CPU baseline by bench.py and checked
 against the C oracle by tests/test_oracle.py.  The product never imports it.
@@ -12,6 +13,11 @@ what a reference user pays on this host:
   iteration per channel, with a ``.item()`` for each boosted one, for the high
   bits, and ``(x - zero) * scale`` in fp32.
 * ``dequantize_value_page`` follows ``kitty/kernels/quantize_value.py:97-133``.
+* ``quantize_key_page`` follows ``kitty/kernels/quantize_key.py:38-124``: fp32
+  per-channel min / max, range clamped to 1e-8, INT4 or INT2 per channel,
+  rounded codes, four codes per byte, then one Python iteration with an
+  ``.item()`` per boosted channel for the high bits; ``quantize_value_page``
+  follows ``kitty/kernels/quantize_value.py:38-90`` (per token, INT2).
 * ``paged_attention`` follows ``kitty/kernels/attention.py:46-189``: the first
   pass over every (page, head), whose dequantised blocks are thrown away
   (lines 100-132), the per-head rebuild of K and V from sinks, pages and
@@ -115,3 +121,48 @@ def paged_attention(q: torch.Tensor, page_list: Sequence[int], key_baseline: tor
         w = torch.softmax((qf[qh] @ K.T) * scale, dim=0)
         rows.append((w.unsqueeze(1) * V).sum(dim=0))
     return torch.stack(rows, 0).to(torch.float16)
+
+
+def _pack4(codes: torch.Tensor) -> torch.Tensor:
+    """Four 2-bit codes per byte along the last dimension, code i of a group
+    in bits 2i (quantize_key.py:106-110, quantize_value.py:85-88)."""
+    out = torch.zeros(*codes.shape[:-1], codes.shape[-1] // 4, dtype=torch.uint8)
+    for i in range(4):
+        out |= (codes[..., i::4] << (2 * i)).to(torch.uint8)
+    return out
+
+
+def quantize_key_page(key: torch.Tensor, boost_idx: torch.Tensor, d_boost: int, sentinel: int):
+    """key (D, G) fp16 -> (low codes (D, G/4), high codes (d_boost, G/4) u8,
+    scale (D,) fp16, zero point (D,) fp16), quantize_key.py:69-124."""
+    x = key.float()
+    D, G = x.shape
+    boosted = boost_idx < sentinel
+    lo, hi = x.min(dim=1).values, x.max(dim=1).values
+    mq = torch.where(boosted, torch.tensor(15.0), torch.tensor(3.0))
+    s = (hi - lo).clamp(min=1e-8) / mq
+    z = torch.minimum(torch.maximum((-lo / s).round(), torch.zeros_like(s)), mq)
+    qf = (x / s[:, None]).round() + z[:, None]
+    q = torch.minimum(torch.maximum(qf, torch.zeros_like(qf)), mq[:, None]).to(torch.uint8)
+    low = _pack4(q & 3)
+    high = torch.zeros(d_boost, G // 4, dtype=torch.uint8)
+    hq = (q >> 2) & 3
+    for d in torch.where(boosted)[0]:
+        r = int(boost_idx[d].item())
+        if r < d_boost:
+            for i in range(4):
+                high[r] |= (hq[d, i::4] << (2 * i)).to(torch.uint8)
+    return low, high, s.to(torch.float16), z.to(torch.float16)
+
+
+def quantize_value_page(value: torch.Tensor):
+    """value (G, D) fp16 -> (codes (G, D/4) u8, scale (G,) fp16, zero point
+    (G,) fp16), quantize_value.py:58-90."""
+    x = value.float()
+    lo, hi = x.min(dim=1).values, x.max(dim=1).values
+    s = (hi - lo).clamp(min=1e-8) / 3.0
+    three = torch.full_like(s, 3.0)
+    z = torch.minimum(torch.maximum((-lo / s).round(), torch.zeros_like(s)), three)
+    qf = (x / s[:, None]).round() + z[:, None]
+    q = torch.minimum(torch.maximum(qf, torch.zeros_like(qf)), torch.full_like(qf, 3.0)).to(torch.uint8)
+    return _pack4(q), s.to(torch.float16), z.to(torch.float16)

@@ -316,6 +316,34 @@ def test_torch_restatement_matches_c_oracle():
     assert (empty.float() == 0).all()
 
 
+def test_torch_quantizers_match_c_oracle():
+    """The torch restatements of quantize_key_page_torch /
+    quantize_value_page_torch (timed as config 2's CPU baseline) give the C
+    oracle's codes, scales and zero points bit for bit: outlier and plain
+    channels, a constant key channel and value token, an all-zero token,
+    boost ranks with a gap and one at the last rank."""
+    import torch_reference as TR
+    rng = np.random.default_rng(33)
+    D, G, dk = 128, 128, 16
+    for trial in range(4):
+        key = (rng.standard_normal((D, G)) * rng.choice([1.0, 8.0], size=(D, 1))).astype(np.float16)
+        key[5] = np.float16(0.75)                           # a constant channel
+        bi = np.full(D, dk + 1, np.uint8)
+        ranks = rng.permutation(dk)[:dk - trial]             # a gap in the ranks for trial > 0
+        bi[rng.permutation(D)[:len(ranks)]] = ranks
+        val = rng.standard_normal((G, D)).astype(np.float16)
+        val[3] = np.float16(-1.5)                            # a constant token
+        val[9] = 0                                           # an all-zero token
+        want_k = O.quantize_key(key, bi, dk, dk + 1)
+        got_k = TR.quantize_key_page(torch.from_numpy(key), torch.from_numpy(bi), dk, dk + 1)
+        for w, g in zip(want_k, got_k):
+            assert np.array_equal(np.asarray(w).view(np.uint8), g.numpy().view(np.uint8)), trial
+        want_v = O.quantize_value(val)
+        got_v = TR.quantize_value_page(torch.from_numpy(val))
+        for w, g in zip(want_v, got_v):
+            assert np.array_equal(np.asarray(w).view(np.uint8), g.numpy().view(np.uint8)), trial
+
+
 @pytest.mark.parametrize("npk,npv,nk", [(4, 4, 5), (4, 2, 5), (3, 0, 0), (5, 3, 7)])
 def test_split_stream_oracle(npk, npv, nk):
     """Independent key / value streams (a value local window): the first npv
