@@ -217,6 +217,23 @@ class KittyInferencePipeline:
         keys = keys.to(self.device, self._dtype)
         values = values.to(self.device, self._dtype)
         l = layer_id
+        append = self._append_device if self._store is not None else self._append_host
+        if len(slots) == 1:
+            # one sequence (push_token): the same steps on scalar counters
+            s = int(slots[0])
+            in_sink = self._fill[s, l] < S
+            kf = not in_sink and self._qlen[s, l] + 1 == G
+            vf = not in_sink and self._vlen[s, l] + 1 == self.value_capacity
+            phys = self._alloc_spill(l, slots, [ids[0]]) if kf else []
+            append(l, keys, values, slots)
+            if in_sink:
+                self._fill[s, l] += 1
+            else:
+                self._qlen[s, l] += 1
+                self._vlen[s, l] += 1
+            if kf or vf:
+                self._spill(l, slots if kf else slots[:0], phys, slots if vf else slots[:0])
+            return
         fill = self._fill[slots, l]
         in_sink = fill < S
         rows = np.nonzero(~in_sink)[0]
@@ -225,10 +242,7 @@ class KittyInferencePipeline:
         kfull = rows[self._qlen[slots[rows], l] + 1 == G]
         vfull = rows[self._vlen[slots[rows], l] + 1 == self.value_capacity]
         phys = self._alloc_spill(l, slots[kfull], [seq_ids[i] for i in kfull]) if len(kfull) else []
-        if self._store is not None:
-            self._append_device(l, keys, values, slots)
-        else:
-            self._append_host(l, keys, values, slots)
+        append(l, keys, values, slots)
         self._fill[slots[in_sink], l] += 1
         self._qlen[slots[rows], l] += 1
         self._vlen[slots[rows], l] += 1
