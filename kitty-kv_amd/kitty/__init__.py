@@ -1,8 +1,10 @@
 """Kitty 2-bit KV cache, MI355X (gfx950) implementation of the quantized-KV hot path.
 
-Public names follow the reference package (kitty/__init__.py:7-27).  All
-compute runs in libkitty_hip.so (hand-written HIP kernels for gfx950) on ROCm
-device tensors; there is no CPU compute path.
+Public names follow the reference package (kitty/__init__.py:7-27).  On ROCm
+device tensors all compute runs in libkitty_hip.so (hand-written HIP kernels
+for gfx950), with no fallback; CPU tensors (the reference's CPU path,
+``KittyConfig.device = "cpu"``) run vectorised torch code
+(``kitty.kernels.cpu``).
 """
 from .config import KittyConfig
 from .layout import Page, PageCentricKVLayoutManager

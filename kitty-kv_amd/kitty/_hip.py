@@ -1,8 +1,9 @@
 """ctypes binding of libkitty_hip.so (C ABI declared in include/kitty_hip.h).
 
-The library is the only compute path of this package: if it is missing, or a
-tensor is not on a ROCm device, calls raise instead of falling back to CPU
-code.  Error codes map to the exception types the reference raises on the
+The library is the only compute path of this package for device tensors:
+if it is missing, calls on device tensors raise instead of falling back to
+CPU code (CPU tensors are dispatched by the callers to ``kernels.cpu``
+before anything here runs).  Error codes map to the exception types the reference raises on the
 same conditions (RuntimeError for an exhausted pool, KeyError for a missing
 page, ValueError/AssertionError-like ValueError for bad shapes).
 """
@@ -140,7 +141,7 @@ def load() -> ctypes.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ImportError(
             f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
-            "(or `make -C kitty-kv_amd/csrc`). There is no CPU fallback.")
+            "(or `make -C kitty-kv_amd/csrc`). Device tensors have no CPU fallback.")
     L = ctypes.CDLL(LIB_PATH)
     L.kitty_abi_version.restype = ctypes.c_int
     L.kitty_last_error.restype = ctypes.c_char_p
@@ -183,7 +184,8 @@ def check(rc: int) -> None:
 
 
 def require_device(*tensors: torch.Tensor) -> torch.device:
-    """All tensors must live on the same ROCm device: no CPU fallback exists."""
+    """All tensors must live on the same ROCm device: the HIP path never
+    falls back to the CPU (CPU inputs are dispatched before this check)."""
     dev = None
     for t in tensors:
         if t is None:

@@ -21,6 +21,10 @@ launch per sequence; the same state as pushing the tokens one at a time,
 which is what the reference does, ``:169-177``), and the output is causal
 attention over the chunk, as the reference computes it (``:179-191``); it
 runs in float32 (torch's SDPA math path).
+
+Pools and buffers on the CPU (``KittyConfig.device = "cpu"``, the reference's
+config-1 plumbing case) run the same steps with the torch code of
+``kernels.cpu``; device pools only ever run the HIP kernels.
 """
 from __future__ import annotations
 
@@ -34,7 +38,7 @@ import torch.nn.functional as F
 from .config import KittyConfig
 from .layout import PageCentricKVLayoutManager
 from .pipeline import KittyInferencePipeline
-from .kernels.ops import DecodePlan, boost_rows_unique
+from .kernels.ops import DecodePlan, boost_rows_unique, decode_plan
 
 
 class KittyPagedAttention(nn.Module):
@@ -78,7 +82,7 @@ class KittyPagedAttention(nn.Module):
             return plan
         x = self.pipeline.decode_inputs(self.layer_id, seq_ids, full_width=True)
         lay = self.layout
-        plan = DecodePlan(qd, x["block_table"], x["num_pages"], lay.key_baseline, lay.key_boost, lay.key_metadata,
+        plan = decode_plan(qd, x["block_table"], x["num_pages"], lay.key_baseline, lay.key_boost, lay.key_metadata,
                           lay.value_pool, lay.value_metadata, self.pipeline.boost_idx_uint8[self.layer_id],
                           x["sink_k"], x["sink_v"], x["sink_len"], x["tail_k"], x["tail_v"], x["tail_len"],
                           max_pages=x["max_pages"], sm_scale=self.scale, boost_unique=self._boost_unique,

@@ -1,7 +1,9 @@
 """Paged decode attention (reference ``kitty/kernels/attention.py``).
 
 ``paged_attention`` keeps the reference signature (one sequence, page list,
-pools, FP16 sinks and Q-buffer tail) and runs the fused split-K HIP kernel;
+pools, FP16 sinks and Q-buffer tail) and runs the fused split-K HIP kernel on
+device tensors, the torch code of ``kernels.cpu`` on CPU tensors (the
+reference's dispatch by device, ``kernels/attention.py:320-341``);
 ``paged_attention_batched`` is the batched entry point (B sequences, int32
 page table) that the drop-in module and the benchmark use.
 """
@@ -12,6 +14,7 @@ from typing import List
 import torch
 
 from .. import _hip
+from . import cpu
 from .ops import _need, paged_decode
 
 
@@ -26,14 +29,17 @@ def paged_attention(q: torch.Tensor, page_list: List[int], key_baseline: torch.T
     attended only when qbuf_k is non-empty, and then K and V tails must have
     the same length (attention.py:163-165; the reference fails in its
     broadcast otherwise, which is raised here as RuntimeError)."""
-    dev = _hip.require_device(q, key_baseline, sink_k, qbuf_k)
     _need(q.shape == (num_q_heads, head_dim), "q must be (num_q_heads, head_dim)")
     _need(key_boost.shape[2] == D_boost, "D_boost does not match key_boost")
-    H = num_kv_heads
     n_tail = qbuf_k.shape[1]
     if n_tail > 0 and qbuf_v.shape[1] != n_tail:
         raise RuntimeError(f"key tail has {n_tail} tokens but value tail has {qbuf_v.shape[1]}; "
                            "the reference requires equal lengths (attention.py:163-165,186)")
+    if q.device.type == "cpu":
+        return cpu.paged_attention(q, page_list, key_baseline, key_boost, key_meta, value_pool, value_meta,
+                                   boost_idx, D_boost, sink_k, sink_v, qbuf_k, qbuf_v, num_q_heads, num_kv_heads,
+                                   head_dim)
+    dev = _hip.require_device(q, key_baseline, sink_k, qbuf_k)
     n_sink = sink_k.shape[1]
     pages = torch.tensor(list(page_list) or [0], dtype=torch.int32).to(dev).view(1, -1)
     lens = torch.tensor([len(page_list), n_sink, n_tail], dtype=torch.int32).to(dev)
@@ -46,7 +52,8 @@ def paged_attention(q: torch.Tensor, page_list: List[int], key_baseline: torch.T
     return out.view(num_q_heads, head_dim)
 
 
-# The reference's CPU reference path is this same kernel here: no CPU path exists.
+# The reference's name for its CPU path (kernels/attention.py:46-189): the same
+# dispatch, so CPU tensors run the torch code and device tensors the kernel.
 paged_attention_reference = paged_attention
 
 paged_attention_batched = paged_decode

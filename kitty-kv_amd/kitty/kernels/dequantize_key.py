@@ -1,7 +1,8 @@
 """Key page dequantisation (reference ``kitty/kernels/dequantize_key.py``):
 k = ((low | high << 2) - z) * s, high bits read from row boost_idx[d] of
 Tensor_High_2bits when boost_idx[d] < D_boost.  HIP kernel
-``dequantize_key_kernel``."""
+``dequantize_key_kernel`` for device tensors, ``kernels.cpu`` for CPU
+tensors."""
 from __future__ import annotations
 
 import ctypes
@@ -9,6 +10,7 @@ import ctypes
 import torch
 
 from .. import _hip
+from . import cpu
 from .ops import _need
 from .quantize_key import _key_store
 
@@ -18,9 +20,15 @@ def dequantize_key_page(tensor_2bits: torch.Tensor, tensor_high_2bits: torch.Ten
                         out: torch.Tensor) -> None:
     """Dequantise one key page into ``out`` (D, G) of float16, bfloat16 or
     float32 (dequantize_key.py:169-228: the fp32 result converted to out's
-    dtype)."""
-    dev = _hip.require_device(tensor_2bits, tensor_high_2bits, scale, zero_point, boost_idx, out)
+    dtype).  A CPU page is dequantised by ``kernels.cpu`` and copied into out
+    wherever it lives."""
     D, G4 = tensor_2bits.shape
+    if tensor_2bits.device.type == "cpu":
+        _need(out.shape == (D, G4 * 4), "out must be (D, G)")
+        out.copy_(cpu.dequantize_key_blocks(tensor_2bits, tensor_high_2bits, scale, zero_point, boost_idx.cpu(),
+                                            D_boost))
+        return
+    dev = _hip.require_device(tensor_2bits, tensor_high_2bits, scale, zero_point, boost_idx, out)
     kinds = {torch.float16: _hip.KITTY_OUT_F16, torch.float32: _hip.KITTY_OUT_F32,
              torch.bfloat16: _hip.KITTY_OUT_BF16}
     _need(out.shape == (D, G4 * 4) and out.stride(1) == 1 and out.dtype in kinds,
@@ -35,7 +43,10 @@ def dequantize_key_page(tensor_2bits: torch.Tensor, tensor_high_2bits: torch.Ten
 
 def dequantize_key_page_torch(tensor_2bits: torch.Tensor, tensor_high_2bits: torch.Tensor, scale: torch.Tensor,
                               zero_point: torch.Tensor, boost_idx: torch.Tensor, D_boost: int) -> torch.Tensor:
-    """(D, G) float32, same signature as dequantize_key.py:35-97, on the device."""
+    """(D, G) float32, same signature as dequantize_key.py:35-97, on the
+    page's device (by ``kernels.cpu`` on the CPU)."""
+    if tensor_2bits.device.type == "cpu":
+        return cpu.dequantize_key_blocks(tensor_2bits, tensor_high_2bits, scale, zero_point, boost_idx, D_boost)
     D, G4 = tensor_2bits.shape
     out = torch.empty(D, G4 * 4, dtype=torch.float32, device=tensor_2bits.device)
     dequantize_key_page(tensor_2bits, tensor_high_2bits, scale, zero_point, boost_idx, D_boost, out)

@@ -2,7 +2,10 @@
 
 Every function here validates shapes/dtypes/devices on the host, builds the
 plain-C argument structs from tensor pointers and strides, and launches on the
-caller's current HIP stream.  Nothing here computes on the CPU.
+caller's current HIP stream.  CPU tensors are dispatched by device to the
+torch code of ``kernels.cpu`` (:func:`quantize_into_pools` with a
+``cpu.PoolSet``, :func:`decode_plan`); device tensors only ever reach the
+HIP library.
 """
 from __future__ import annotations
 
@@ -14,6 +17,7 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from .. import _hip
+from . import cpu
 
 
 def _need(cond: bool, msg: str) -> None:
@@ -121,6 +125,7 @@ def quantize_into_pools(store: _hip.PageStore, key: Optional[torch.Tensor], valu
                         boost_idx: Optional[torch.Tensor], page_ids: torch.Tensor, sentinel: int,
                         value_rows: Optional[int] = None) -> None:
     """One launch over an (outer, inner=head) grid of fp16 or bf16 blocks.
+    A ``cpu.PoolSet`` store (pools on the CPU) runs ``cpu.quantize_into_pools``.
 
     key / value: (n_outer, n_inner, G, D) fp16 or bf16 views (any strides),
     or (n_seq, n_per, n_inner, G, D) views whose n_seq * n_per blocks are
@@ -128,6 +133,9 @@ def quantize_into_pools(store: _hip.PageStore, key: Optional[torch.Tensor], valu
     place); boost_idx: (n_outer, n_inner, D) or (n_inner, D) uint8;
     page_ids: (n_outer,) int32 device tensor of destination pages.
     """
+    if isinstance(store, cpu.PoolSet):
+        cpu.quantize_into_pools(store, key, value, boost_idx, page_ids, sentinel, value_rows)
+        return
     b, dev = _quant_batch(store, key, value, boost_idx, page_ids, sentinel, value_rows)
     _hip.check(_hip.load().kitty_quantize_kv_blocks(ctypes.byref(store), ctypes.byref(b), _hip.stream_ptr(dev)))
 
@@ -317,9 +325,18 @@ def _warn_generic(boost_unique: bool, act_dtype: int, meta_dtype: int) -> None:
                   "15x slower than the MFMA kernel", RuntimeWarning, stacklevel=3)
 
 
+def decode_plan(*args, **kwargs):
+    """``DecodePlan`` for device tensors, ``cpu.CpuDecodePlan`` (same
+    arguments and methods) when q is a CPU tensor."""
+    q = args[0] if args else kwargs["q"]
+    if q.device.type == "cpu":
+        return cpu.CpuDecodePlan(*args, **kwargs)
+    return DecodePlan(*args, **kwargs)
+
+
 def paged_decode(*args, **kwargs) -> torch.Tensor:
-    """Batched fused paged decode attention: ``DecodePlan(*args, **kwargs).run()``."""
-    return DecodePlan(*args, **kwargs).run()
+    """Batched fused paged decode attention: ``decode_plan(*args, **kwargs).run()``."""
+    return decode_plan(*args, **kwargs).run()
 
 
 def decode_workspace_bytes(B: int, Hq: int, Hkv: int, D: int, G: int, Dk: int, max_pages: int,

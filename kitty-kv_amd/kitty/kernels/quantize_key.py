@@ -4,8 +4,9 @@ Per-channel min-max over the G tokens of a page, INT4 for boosted channels
 (``boost_idx[d] < sentinel``) and INT2 otherwise, packed into the dense-sparse
 layout: low 2 bits of every channel -> ``Tensor_2bits`` (D, G/4), high 2 bits
 of boosted channels -> row ``boost_idx[d]`` of ``Tensor_High_2bits``
-(D_boost, G/4).  Computed by the HIP kernel ``quantize_kv_kernel``; results
-are bit-identical to the reference's ``quantize_key_page_torch``.
+(D_boost, G/4).  Computed by the HIP kernel ``quantize_kv_kernel`` for device
+tensors and by ``kernels.cpu`` for CPU tensors; results are bit-identical to
+the reference's ``quantize_key_page_torch``.
 """
 from __future__ import annotations
 
@@ -14,6 +15,7 @@ from typing import Tuple
 import torch
 
 from .. import _hip
+from . import cpu
 from .ops import _dtype16, _need, quantize_into_pools
 
 
@@ -42,10 +44,17 @@ def quantize_key_page(key: torch.Tensor, boost_idx: torch.Tensor, D_boost: int, 
     """Quantise one (D, G) fp16 or bf16 key block into pre-allocated outputs
     (reference quantize_key.py:217-269); float16 or bfloat16 out_scale /
     out_zero receive the fp16 scale and zero point converted to their dtype,
-    as the reference's copy_ does."""
-    dev = _hip.require_device(key, boost_idx, out_baseline, out_boost, out_scale, out_zero)
+    as the reference's copy_ does.  A CPU key is quantised by the torch code
+    of ``kernels.cpu`` and copied into the outputs wherever they live
+    (quantize_key.py:263-269)."""
     D, G = key.shape
     assert G % 4 == 0, "G must be divisible by 4 for uint8 packing"
+    if key.device.type == "cpu":
+        res = cpu.quantize_key_blocks(key, boost_idx.cpu(), D_boost, sentinel)
+        for out, r in zip((out_baseline, out_boost, out_scale, out_zero), res):
+            out.copy_(r)
+        return
+    dev = _hip.require_device(key, boost_idx, out_baseline, out_boost, out_scale, out_zero)
     store = _key_store(D, G, D_boost, out_baseline, out_boost, out_scale, out_zero)
     page0 = torch.zeros(1, dtype=torch.int32, device=dev)
     quantize_into_pools(store, key.t()[None, None], None, boost_idx.reshape(1, D), page0, sentinel)
@@ -54,7 +63,10 @@ def quantize_key_page(key: torch.Tensor, boost_idx: torch.Tensor, D_boost: int, 
 def quantize_key_page_torch(key: torch.Tensor, boost_idx: torch.Tensor, D_boost: int,
                             sentinel: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """Same signature and outputs as the reference's pure-PyTorch quantiser
-    (quantize_key.py:38-124), computed by the HIP kernel on the key's device."""
+    (quantize_key.py:38-124), computed by the HIP kernel on the key's device
+    (by ``kernels.cpu`` for a CPU key)."""
+    if key.device.type == "cpu":
+        return cpu.quantize_key_blocks(key, boost_idx.cpu(), D_boost, sentinel)
     _hip.require_device(key, boost_idx)
     D, G = key.shape
     dev = key.device

@@ -2,7 +2,8 @@
 
 Per-token INT2 min-max over D channels, 4 channels per byte along D, with a
 per-token fp16 (scale, zero point).  Computed by the HIP kernel
-``quantize_kv_kernel``; bit-identical to ``quantize_value_page_torch``.
+``quantize_kv_kernel`` for device tensors and by ``kernels.cpu`` for CPU
+tensors; bit-identical to ``quantize_value_page_torch``.
 """
 from __future__ import annotations
 
@@ -12,6 +13,7 @@ from typing import Tuple
 import torch
 
 from .. import _hip
+from . import cpu
 from .ops import _dtype16, _need, quantize_into_pools
 
 
@@ -34,17 +36,25 @@ def quantize_value_page(value: torch.Tensor, out_packed: torch.Tensor, out_scale
                         out_zero: torch.Tensor) -> None:
     """Quantise one (G, D) fp16 or bf16 value block into pre-allocated
     outputs; the scale / zero views (float16 or bfloat16) may be strided
-    (quantize_value.py:197-227)."""
-    dev = _hip.require_device(value, out_packed, out_scale, out_zero)
+    (quantize_value.py:197-227).  A CPU value block is quantised by
+    ``kernels.cpu`` and copied into the outputs wherever they live."""
     G, D = value.shape
     assert D % 4 == 0, "head_dim D must be divisible by 4 for packing"
+    if value.device.type == "cpu":
+        for out, r in zip((out_packed, out_scale, out_zero), cpu.quantize_value_blocks(value)):
+            out.copy_(r)
+        return
+    dev = _hip.require_device(value, out_packed, out_scale, out_zero)
     store = _value_store(G, D, out_packed, out_scale, out_zero)
     page0 = torch.zeros(1, dtype=torch.int32, device=dev)
     quantize_into_pools(store, None, value[None, None], None, page0, 0)
 
 
 def quantize_value_page_torch(value: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Same signature and outputs as quantize_value.py:38-90, computed on the device."""
+    """Same signature and outputs as quantize_value.py:38-90, computed on the
+    value's device (by ``kernels.cpu`` for a CPU block)."""
+    if value.device.type == "cpu":
+        return cpu.quantize_value_blocks(value)
     _hip.require_device(value)
     G, D = value.shape
     dev = value.device
@@ -56,7 +66,10 @@ def quantize_value_page_torch(value: torch.Tensor) -> Tuple[torch.Tensor, torch.
 
 
 def dequantize_value_page_torch(packed: torch.Tensor, scale: torch.Tensor, zero_point: torch.Tensor) -> torch.Tensor:
-    """(G, D) float32 values, (code - z_t) * s_t (quantize_value.py:97-133), on the device."""
+    """(G, D) float32 values, (code - z_t) * s_t (quantize_value.py:97-133),
+    on the device of the packed page (by ``kernels.cpu`` on the CPU)."""
+    if packed.device.type == "cpu":
+        return cpu.dequantize_value_blocks(packed, scale, zero_point)
     dev = _hip.require_device(packed, scale, zero_point)
     G, D4 = packed.shape
     out = torch.empty(G, D4 * 4, dtype=torch.float32, device=dev)

@@ -58,6 +58,7 @@ import torch
 from . import _hip
 from .config import KittyConfig
 from .layout import PageCentricKVLayoutManager
+from .kernels import cpu
 from .kernels.ops import pool_store, quantize_into_pools
 
 _FILL, _QLEN, _NPAGES, _NPAGES_V, _VLEN = 0, 1, 2, 3, 4
@@ -109,12 +110,15 @@ class KittyInferencePipeline:
         self._slots_of_ids: Dict[Tuple[int, ...], np.ndarray] = {}
         # append arguments per (layer, slots): everything but the token pointers
         self._append_args: Dict[Tuple[int, Tuple[int, ...]], Tuple[_hip.AppendArgs, torch.Tensor]] = {}
-        self._store = None
         self._lib = None
-        if dev.type == "cuda":
+        self._on_device = dev.type == "cuda"
+        if self._on_device:
             self._lib = _hip.load()
             self._store = pool_store(layout.key_baseline, layout.key_boost, layout.key_metadata,
                                      layout.value_pool, layout.value_metadata)
+        else:   # pools on the CPU: spills run the torch code of kernels.cpu
+            self._store = cpu.PoolSet(layout.key_baseline, layout.key_boost, layout.key_metadata,
+                                      layout.value_pool, layout.value_metadata)
 
     # ------------------------------------------------------------- slots
     def slot(self, seq_id: int) -> int:
@@ -217,7 +221,7 @@ class KittyInferencePipeline:
         keys = keys.to(self.device, self._dtype)
         values = values.to(self.device, self._dtype)
         l = layer_id
-        append = self._append_device if self._store is not None else self._append_host
+        append = self._append_device if self._on_device else self._append_host
         if len(slots) == 1:
             # one sequence (push_token): the same steps on scalar counters
             s = int(slots[0])
@@ -290,8 +294,9 @@ class KittyInferencePipeline:
         return a, slots_dev
 
     def _append_host(self, l: int, keys: torch.Tensor, values: torch.Tensor, slots: np.ndarray) -> None:
-        """Buffer bookkeeping without a ROCm device (the FP16 buffers only;
-        spilling needs the HIP kernels)."""
+        """The token append for buffers on the CPU: the same routing as
+        kitty_append_tokens (sink while it has room, else key and value
+        buffers), one sequence at a time."""
         S = self.config.sink_size
         fill = self._fill[slots, l]
         for i, s in enumerate(slots.tolist()):
@@ -315,8 +320,6 @@ class KittyInferencePipeline:
         of them, default one each), all or nothing: on a full pool or a
         sequence past max_seq_len the pages already taken are returned and
         RuntimeError is raised."""
-        if self._store is None:
-            raise RuntimeError("kitty (MI355X build) quantises only on ROCm devices")
         taken: List[Tuple[int, int, List[int]]] = []   # (seq, first page number, its run)
         try:
             for i, (s, seq) in enumerate(zip(np.asarray(slots).tolist(), seq_ids)):
@@ -402,18 +405,26 @@ class KittyInferencePipeline:
         T = keys.shape[2]
         l = layer_id
         slots = np.array([self.slot(seq) for seq in seq_ids], dtype=np.int64)
-        fresh = not self._counts[:, slots, l].any()
-        if fresh and self._store is not None and len(set(slots.tolist())) == len(slots):
+        if len(set(slots.tolist())) != len(slots):
+            raise ValueError("a sequence appears twice in one push")
+        if not self._counts[:, slots, l].any():
             self._push_chunk_fresh(l, keys, values, slots, seq_ids)
             return
+        # every sequence's new key pages, all or nothing, before any state
+        # changes: a full pool raises with the batch untouched
+        fills = self._fill[slots, l]
+        n_sink = np.where(fills < S, np.minimum(T, S - fills), 0)
+        n_fulls = np.where(T > n_sink, (self._qlen[slots, l] + T - n_sink) // G, 0)
+        need = np.nonzero(n_fulls)[0]
+        phys_all = self._alloc_spill(l, slots[need], [seq_ids[i] for i in need], n_fulls[need]) if len(need) else []
+        runs = np.split(np.asarray(phys_all, np.int64), np.cumsum(n_fulls[need])[:-1]) if len(need) else []
+        phys_of = dict(zip(need.tolist(), runs))
         for i, seq in enumerate(seq_ids):
-            s = self.slot(seq)
+            s = int(slots[i])
             t = 0
             f = int(self._fill[s, l])
-            n_s = min(T, S - f) if f < S else 0
-            # the chunk's new key pages, all or nothing, before any state changes
-            n_full = (int(self._qlen[s, l]) + T - n_s) // G if T > n_s else 0
-            phys = self._alloc_spill(l, np.array([s]), [seq], [n_full]) if n_full else []
+            n_s, n_full = int(n_sink[i]), int(n_fulls[i])
+            phys = phys_of.get(i, [])
             if n_s:
                 self._sink_k[s, l, :, f:f + n_s] = keys[i, :, :n_s]
                 self._sink_v[s, l, :, f:f + n_s] = values[i, :, :n_s]

@@ -12,7 +12,8 @@ with the reference:
     meta.json       config snapshot and calibration token counts per layer
 
 The per-(head, channel) sum of |k| is accumulated on the ROCm device by
-``kitty_channel_abs_sum`` (fixed summation order).  Ranks come from a stable
+``kitty_channel_abs_sum`` (fixed summation order); keys on the CPU are summed
+with torch there.  Ranks come from a stable
 descending sort, so equal scores rank by channel index; the reference's
 ``argsort`` leaves the order of ties unspecified.
 """
@@ -56,10 +57,15 @@ class _ChannelAccumulator:
 
     @torch.no_grad()
     def update(self, key: torch.Tensor) -> None:
-        """key (batch, num_kv_heads, seq_len, head_dim) fp16 / bf16 on the ROCm device."""
+        """key (batch, num_kv_heads, seq_len, head_dim) fp16 / bf16 on the ROCm
+        device (a CPU key is summed with torch on the CPU)."""
         B, H, T, D = key.shape
         if (H, D) != (self.num_kv_heads, self.head_dim):
             raise ValueError(f"key shape {tuple(key.shape)} does not match ({self.num_kv_heads}, {self.head_dim})")
+        if key.device.type == "cpu":
+            self._sum_abs = self.sum_abs.cpu() + key.abs().float().sum(dim=(0, 2))
+            self.token_count += B * T
+            return
         dev = _hip.require_device(key)
         if self._sum_abs.device != dev:
             self._sum_abs = self.sum_abs.to(dev)      # pending slots flushed on the old device first

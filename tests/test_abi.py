@@ -90,18 +90,49 @@ def test_workspace_size_formula():
     assert decode_workspace_bytes(16, 16, 8, 128, 128, 16, 255) == 16 * 16 * 16 * row
 
 
-def test_cpu_tensors_rejected_no_fallback():
+def test_hip_boundary_rejects_cpu_tensors():
+    """The HIP path never computes on the CPU: its device check refuses CPU
+    tensors (the public functions dispatch CPU tensors to kernels.cpu before
+    it), and a DecodePlan built directly over CPU tensors raises."""
     import torch
-    from kitty.kernels import quantize_value_page_torch, paged_attention
+    from kitty import _hip
+    from kitty.kernels.ops import DecodePlan
     with pytest.raises(RuntimeError, match="ROCm device"):
-        quantize_value_page_torch(torch.zeros(8, 16, dtype=torch.float16))
+        _hip.require_device(torch.zeros(4, dtype=torch.float16))
+    z8 = torch.zeros(1, 1, 16, 2, dtype=torch.uint8)
+    i1 = torch.zeros(1, dtype=torch.int32)
     with pytest.raises(RuntimeError, match="ROCm device"):
-        z8 = torch.zeros(1, 1, 16, 2, dtype=torch.uint8)
-        paged_attention(torch.zeros(1, 16, dtype=torch.float16), [], z8, z8[:, :, :0], torch.zeros(1, 1, 2, 16).half(),
-                        torch.zeros(1, 1, 8, 4, dtype=torch.uint8), torch.zeros(1, 1, 8, 2).half(),
-                        torch.zeros(1, 16, dtype=torch.uint8), 0, torch.zeros(1, 0, 16).half(),
-                        torch.zeros(1, 0, 16).half(), torch.zeros(1, 0, 16).half(), torch.zeros(1, 0, 16).half(),
-                        1, 1, 16)
+        DecodePlan(torch.zeros(1, 1, 16).half(), torch.zeros(1, 1, dtype=torch.int32), i1, z8, z8[:, :, :0],
+                   torch.zeros(1, 1, 2, 16).half(), torch.zeros(1, 1, 8, 4, dtype=torch.uint8),
+                   torch.zeros(1, 1, 8, 2).half(), torch.zeros(1, 16, dtype=torch.uint8),
+                   *(torch.zeros(1, 1, 0, 16).half(),) * 2, i1, *(torch.zeros(1, 1, 0, 16).half(),) * 2, i1)
+
+
+def test_cpu_dispatch_never_loads_the_hip_library():
+    """CPU tensors run kitty.kernels.cpu without the HIP library, while any
+    device call needs it: with the library path pointing nowhere, CPU calls
+    work and loading the library raises ImportError (no fallback)."""
+    import subprocess
+    import sys
+    code = (
+        "import sys, torch; sys.path.insert(0, %r)\n"
+        "from kitty import _hip\n"
+        "from kitty.kernels import quantize_value_page_torch, paged_attention\n"
+        "p, s, z = quantize_value_page_torch(torch.full((8, 16), 3.0).half())\n"
+        "assert (p == 0xFF).all()\n"
+        "z8 = torch.zeros(1, 1, 16, 2, dtype=torch.uint8)\n"
+        "out = paged_attention(torch.zeros(1, 16).half(), [], z8, z8[:, :, :0], torch.zeros(1, 1, 2, 16).half(),"
+        " torch.zeros(1, 1, 8, 4, dtype=torch.uint8), torch.zeros(1, 1, 8, 2).half(),"
+        " torch.zeros(1, 16, dtype=torch.uint8), 0, torch.ones(1, 2, 16).half(), torch.ones(1, 2, 16).half(),"
+        " torch.zeros(1, 0, 16).half(), torch.zeros(1, 0, 16).half(), 1, 1, 16)\n"
+        "assert (out == 1).all()\n"
+        "assert _hip._lib is None\n"
+        "try:\n    _hip.load()\nexcept ImportError as e:\n    print('no-lib', 'no CPU fallback' in str(e))\n"
+    ) % os.path.join(ROOT, "kitty-kv_amd")
+    env = dict(os.environ, KITTY_HIP_LIBRARY=os.path.join(ROOT, "no_such_library.so"))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120, env=env)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.strip() == "no-lib True"
 
 
 def test_bench_refuses_more_than_one_gpu():

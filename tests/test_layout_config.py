@@ -144,9 +144,9 @@ def test_pool_override_sizes_multi_layer_pools():
     assert lay.key_baseline.shape[0] == cfg.max_pages * 2
 
 
-def test_pipeline_counters_on_cpu_and_no_cpu_quantisation():
-    """Host bookkeeping works anywhere; a spill needs the HIP kernels and a
-    ROCm device (there is no CPU fallback)."""
+def test_pipeline_counters_on_cpu():
+    """Host bookkeeping and the CPU pipeline: sinks, buffers and a spill into
+    a page on CPU pools (the spill's bytes are pinned in test_cpu_path.py)."""
     from kitty import KittyInferencePipeline
     cfg = _cfg(num_layers=1)
     lay = _layout(cfg)
@@ -158,6 +158,7 @@ def test_pipeline_counters_on_cpu_and_no_cpu_quantisation():
     assert p.sink_fill == cfg.sink_size and p.key_qbuf_len == 3 and p.val_local_len == 3
     ctx = p.get_attention_context(0)
     assert ctx["sink_k"].shape == (H, cfg.sink_size, D) and ctx["key_qbuf"].shape == (H, 3, D)
-    with pytest.raises(RuntimeError, match="ROCm"):
-        for _ in range(cfg.q_buffer_size):
-            p.push_token(0, torch.randn(H, D).half(), torch.randn(H, D).half())
+    for _ in range(cfg.q_buffer_size - 3):
+        p.push_token(0, torch.randn(H, D).half(), torch.randn(H, D).half())
+    assert p.key_qbuf_len == 0 and len(lay.get_page_list(0, 0)) == 1
+    assert lay.key_metadata[lay.get_page_list(0, 0)[0], :, 0].abs().sum() > 0

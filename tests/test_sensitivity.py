@@ -60,11 +60,20 @@ def test_summary_lines():
     assert lines[5] == "  Mean channel score: 2.0000"
 
 
-def test_accumulation_needs_a_rocm_device():
+def test_accumulation_on_cpu_matches_float64():
+    """CPU keys are summed per (head, channel) over batch and tokens: the
+    same scores as float64 sums, then the same ranking."""
     cfg = KittyConfig(num_layers=1, num_kv_heads=2, head_dim=16, device="cpu")
     prof = KittySensitivityProfiler(cfg)
-    with pytest.raises(RuntimeError, match="ROCm"):
-        prof.update(0, torch.zeros(1, 2, 4, 16, dtype=torch.float16))
+    g = torch.Generator().manual_seed(6)
+    keys = [torch.randn(2, 2, 9, 16, generator=g).half() for _ in range(3)]
+    keys[1][:, :, :, 4] *= 16
+    for k in keys:
+        prof.update(0, k)
+    ref = sum(k.double().abs().sum(dim=(0, 2)) for k in keys) / (3 * 2 * 9)
+    assert torch.allclose(prof.accumulator(0).scores().double(), ref, rtol=1e-6)
+    prof.compute()
+    assert (prof.boost_idx_uint8[0, :, 4] == 0).all()
 
 
 @pytest.mark.gpu
