@@ -15,7 +15,7 @@ import torch
 
 from .. import _hip
 from . import cpu
-from .ops import _need, paged_decode
+from .ops import _need, paged_decode, stage_i32
 
 
 def paged_attention(q: torch.Tensor, page_list: List[int], key_baseline: torch.Tensor, key_boost: torch.Tensor,
@@ -41,8 +41,9 @@ def paged_attention(q: torch.Tensor, page_list: List[int], key_baseline: torch.T
                                    head_dim)
     dev = _hip.require_device(q, key_baseline, sink_k, qbuf_k)
     n_sink = sink_k.shape[1]
-    pages = torch.tensor(list(page_list) or [0], dtype=torch.int32).to(dev).view(1, -1)
-    lens = torch.tensor([len(page_list), n_sink, n_tail], dtype=torch.int32).to(dev)
+    # lengths and the page list in one non-blocking copy from pinned staging
+    staged = stage_i32([len(page_list), n_sink, n_tail] + (list(page_list) or [0]), dev)
+    lens, pages = staged[:3], staged[3:].view(1, -1)
     tail_v = qbuf_v if n_tail > 0 else qbuf_k
     out = paged_decode(q.view(1, num_q_heads, head_dim), pages, lens[0:1], key_baseline, key_boost, key_meta,
                        value_pool, value_meta, boost_idx.contiguous(),

@@ -9,11 +9,13 @@ HIP library.
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 import math
 import warnings
 from typing import Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from .. import _hip
@@ -161,15 +163,87 @@ class QuantizePlan:
 
 # --------------------------------------------------------------- decode
 
+_unique_cache: "collections.OrderedDict" = collections.OrderedDict()
+
+
 def boost_rows_unique(boost_idx: torch.Tensor, d_boost: int) -> bool:
-    """True when no rank below d_boost repeats within a boost_idx row (one
-    small device-to-host copy); the MFMA decode path relies on it."""
-    bi = boost_idx.detach().to("cpu", torch.int64).reshape(-1, boost_idx.shape[-1])
+    """True when no rank below d_boost repeats within a boost_idx row; the
+    MFMA decode path relies on it.  Checking reads the rows back to the host
+    (a device-to-host copy, which waits for the stream), so the answer is
+    kept per boost tensor: keyed by its address, shape, strides and torch's
+    version counter (which every in-place write through torch advances),
+    with a reference that keeps the memory from being reused while the
+    entry lives.  Writes that bypass torch (a kernel given the raw pointer)
+    are not seen; pass ``boost_unique`` to the plan in that case."""
+    t = boost_idx.detach()
+    key = (t.device, t.data_ptr(), tuple(t.shape), tuple(t.stride()), t._version, int(d_boost))
+    hit = _unique_cache.get(key)
+    if hit is not None:
+        _unique_cache.move_to_end(key)
+        return hit[1]
+    bi = t.to("cpu", torch.int64).reshape(-1, t.shape[-1])
+    ok = True
     for row in bi:
         ranks = row[row < d_boost]
         if ranks.numel() != torch.unique(ranks).numel():
-            return False
-    return True
+            ok = False
+            break
+    _unique_cache[key] = (t, ok)
+    if len(_unique_cache) > 32:
+        _unique_cache.popitem(last=False)
+    return ok
+
+
+class HostStager:
+    """Small int32 host data onto the device without a blocking copy or a
+    fresh pinned allocation per call: a ring of pinned staging rows,
+    allocated once, and non-blocking copies on the current stream.  A row is
+    rewritten only after the event recorded behind its last copy completed
+    (`ring` copies earlier: in practice never a wait).  Data larger than a
+    row takes a freshly pinned tensor."""
+
+    def __init__(self, device: torch.device, cap: int, ring: int = 8) -> None:
+        self.device = device
+        self._buf = torch.empty(ring, cap, dtype=torch.int32, pin_memory=True)
+        self._np = self._buf.numpy()
+        self._ev: list = [None] * ring
+        self._i = 0
+
+    def __call__(self, a, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """`a` as an int32 device tensor (new, or the front of `out`)."""
+        a = np.ascontiguousarray(a, dtype=np.int32).reshape(-1)
+        n = a.size
+        row = None
+        if n > self._buf.shape[1]:
+            src = torch.from_numpy(a).pin_memory()
+        else:
+            row = self._i
+            self._i = (row + 1) % len(self._ev)
+            if self._ev[row] is not None:
+                self._ev[row].synchronize()
+            self._np[row, :n] = a
+            src = self._buf[row, :n]
+        if out is None:
+            out = src.to(self.device, non_blocking=True)
+        else:
+            out[:n].copy_(src, non_blocking=True)
+        if row is not None:
+            if self._ev[row] is None:
+                self._ev[row] = torch.cuda.Event()
+            self._ev[row].record()
+        return out
+
+
+_stagers: dict = {}
+
+
+def stage_i32(values, device: torch.device) -> torch.Tensor:
+    """int32 host values as a device tensor through the device's shared
+    HostStager (rows of 4096 values)."""
+    st = _stagers.get(device)
+    if st is None:
+        st = _stagers[device] = HostStager(device, 4096)
+    return st(values)
 
 
 class DecodePlan:

@@ -59,7 +59,7 @@ from . import _hip
 from .config import KittyConfig
 from .layout import PageCentricKVLayoutManager
 from .kernels import cpu
-from .kernels.ops import pool_store, quantize_into_pools
+from .kernels.ops import HostStager, QuantizePlan, pool_store, quantize_into_pools
 
 _FILL, _QLEN, _NPAGES, _NPAGES_V, _VLEN = 0, 1, 2, 3, 4
 
@@ -111,6 +111,11 @@ class KittyInferencePipeline:
         # append arguments per (layer, slots): everything but the token pointers
         self._append_args: Dict[Tuple[int, Tuple[int, ...]], Tuple[_hip.AppendArgs, torch.Tensor]] = {}
         self._lib = None
+        self._stager = None         # pinned staging rows of _h2d, allocated on first use
+        self._meta_dev = None       # a spill's staged metadata (fixed address, see _stage_meta)
+        # per (layer, first slot, count, kind): the quantise launch of a spill
+        # of that run of slots, validated once (page ids read from _spill_ids)
+        self._spill_plans: Dict[Tuple[int, int, int, str], object] = {}
         self._on_device = dev.type == "cuda"
         if self._on_device:
             self._lib = _hip.load()
@@ -181,14 +186,18 @@ class KittyInferencePipeline:
         return self._vbuf[self._slot0()]
 
     # ---------------------------------------------------- host -> device
-    def _h2d(self, a) -> torch.Tensor:
+    def _h2d(self, a, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Small int32 host data on the device without a blocking copy: a
-        pinned staging tensor (torch's host cache recycles it once the copy
-        has run) and a non-blocking copy on the current stream."""
-        t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32))
-        if self.device.type != "cuda":
-            return t
-        return t.pin_memory().to(self.device, non_blocking=True)
+        ring of pinned staging rows allocated once (pinning a fresh tensor
+        per call cost ~75 µs of host time) and a non-blocking copy on the
+        current stream into a new device tensor, or into the front of `out`
+        (kernels.ops.HostStager).  A new tensor keeps the shape of `a`."""
+        a = np.ascontiguousarray(a, dtype=np.int32)
+        if not self._on_device:
+            return torch.from_numpy(a)
+        if self._stager is None:
+            self._stager = HostStager(self.device, 16 + 12 * self.num_slots)
+        return self._stager(a, out) if out is not None else self._stager(a).view(a.shape)
 
     def _slots_tensor(self, slots: np.ndarray) -> torch.Tensor:
         key = tuple(int(s) for s in slots)
@@ -342,10 +351,17 @@ class KittyInferencePipeline:
         One launch each; one launch for both when R = 0 (the same slots and
         pages).  The host counters are advanced first; their new values for
         every touched slot travel to the device with the slots and page ids
-        in one pinned copy and land in one indexed write."""
+        in one pinned copy and land in one write.
+
+        Host cost: a run of ascending slots (sequences that advance in
+        lockstep, and every single sequence) quantises through launches
+        validated once per (layer, run) that read their page ids from a fixed
+        device buffer, and updates the block table and counters with slice
+        copies; other slot sets gather their rows and use indexed writes."""
         G, R = self.config.q_buffer_size, self.config.local_value_window
         both = R == 0
         k, v = len(kslots), (0 if both else len(vslots))
+        n = self.num_slots
         pno = self._npages[kslots, layer].copy()
         vphys = self._pages[vslots, layer, self._npv[vslots, layer]] if v else np.zeros(0, np.int64)
         if k:
@@ -361,36 +377,94 @@ class KittyInferencePipeline:
         touched = np.union1d(kslots, vslots[:v]).astype(np.int64)
         lens_new = self._counts[:, touched, layer]
         nt = len(touched)
-        meta = self._h2d(np.concatenate([kslots, pno, np.asarray(phys, np.int64), vslots[:v], vphys, touched,
-                                         lens_new.ravel()]))
-        ksl, kpn, kpages = meta[:k].long(), meta[k:2 * k].long(), meta[2 * k:3 * k]
-        o = 3 * k
-        vsl, vpages = meta[o:o + v].long(), meta[o + v:o + 2 * v]
-        o += 2 * v
-        tsl, lens_dev = meta[o:o + nt].long(), meta[o + nt:o + 6 * nt].view(5, nt)
-        # an ascending run of slots (sequences that advance in lockstep) is
-        # read through a slice view of the buffers, other sets by a gather
-        rows = lambda t, sl, idx: t[int(sl[0]):int(sl[0]) + len(sl)] if _is_run(sl) else t.index_select(0, idx)
+        # staged int32: key page ids at [0, k), value page ids at [n, n + v)
+        # (fixed places the cached launches read), then slots, page numbers
+        # and the touched slots' counters
+        host = np.zeros(2 * n + 3 * k + v + 6 * nt, np.int64)
+        host[:k] = phys
+        host[n:n + v] = vphys
+        o = 2 * n
+        for part in (kslots, pno, vslots[:v], touched, lens_new.ravel()):
+            host[o:o + len(part)] = part
+            o += len(part)
+        meta = self._stage_meta(host)
+        kpages, vpages = meta[:k], meta[n:n + v]
+        o = 2 * n
+        ksl, kpn = meta[o:o + k], meta[o + k:o + 2 * k]
+        vsl = meta[o + 2 * k:o + 2 * k + v]
+        o += 2 * k + v
+        tsl, lens_dev = meta[o:o + nt], meta[o + nt:o + 6 * nt].view(5, nt)
+        sentinel = self.config.sentinel
         if k:
-            kblk = rows(self._qbuf_k[:, layer], kslots, ksl)             # (n, H, G, D)
-            vblk = rows(self._vbuf[:, layer], kslots, ksl)[:, :, :G] if both else None
-            quantize_into_pools(self._store, kblk, vblk, self.boost_idx_uint8[layer], kpages, self.config.sentinel)
-            self._block_table[layer, ksl, kpn] = kpages
+            if _is_run(kslots):
+                a = int(kslots[0])
+                if self._on_device:
+                    self._run_plan(layer, a, k, "kv" if both else "k", meta).run()
+                else:
+                    quantize_into_pools(self._store, self._qbuf_k[a:a + k, layer],
+                                        self._vbuf[a:a + k, layer, :, :G] if both else None,
+                                        self.boost_idx_uint8[layer], kpages, sentinel)
+                if (pno == pno[0]).all():   # sequences in lockstep: one page number
+                    self._block_table[layer, a:a + k, int(pno[0])] = kpages if k > 1 else int(phys[0])
+                else:
+                    self._block_table[layer, ksl, kpn] = kpages
+            else:
+                kblk = self._qbuf_k[:, layer].index_select(0, ksl)
+                vblk = self._vbuf[:, layer].index_select(0, ksl)[:, :, :G] if both else None
+                quantize_into_pools(self._store, kblk, vblk, self.boost_idx_uint8[layer], kpages, sentinel)
+                self._block_table[layer, ksl, kpn] = kpages
         if v:
             vb = self._vbuf[:, layer]                                     # (slots, H, R + G, D)
             if _is_run(vslots[:v]):
                 a = int(vslots[0])
                 vblk = vb[a:a + v]
-                quantize_into_pools(self._store, None, vblk[:, :, :G], None, vpages, self.config.sentinel)
+                if self._on_device:
+                    self._run_plan(layer, a, v, "v", meta).run()
+                else:
+                    quantize_into_pools(self._store, None, vblk[:, :, :G], None, vpages, sentinel)
                 if R:   # the R newest values move to the front, after the launch above read the oldest G
                     src = vblk[:, :, G:G + R]
                     vblk[:, :, :R] = src if R <= G else src.clone()       # overlapping rows need a copy first
             else:
                 vblk = vb.index_select(0, vsl)                            # a copy: the shift below reuses rows
-                quantize_into_pools(self._store, None, vblk[:, :, :G], None, vpages, self.config.sentinel)
+                quantize_into_pools(self._store, None, vblk[:, :, :G], None, vpages, sentinel)
                 if R:
                     vb[vsl, :, :R] = vblk[:, :, G:G + R]                  # the R newest values move to the front
-        self.lens[:, layer, tsl] = lens_dev
+        if _is_run(touched):
+            self.lens[:, layer, int(touched[0]):int(touched[0]) + nt] = lens_dev
+        else:
+            self.lens[:, layer, tsl] = lens_dev
+
+    def _stage_meta(self, host: np.ndarray) -> torch.Tensor:
+        """A spill's int32 metadata on the device, in a buffer of fixed
+        address (the cached launches of _run_plan read their page ids from
+        it), copied straight from the pinned staging ring; stream order keeps
+        a spill's copy behind the previous spill's launches that read it."""
+        if not self._on_device:
+            return self._h2d(host)
+        if self._meta_dev is None:
+            self._meta_dev = torch.zeros(16 + 12 * self.num_slots, dtype=torch.int32, device=self.device)
+        self._h2d(host, out=self._meta_dev)
+        return self._meta_dev
+
+    def _run_plan(self, layer: int, a: int, count: int, kind: str, meta: torch.Tensor):
+        """The quantise launch of a spill of slots [a, a + count) at a layer:
+        "k" (keys into the pages at meta[0:count]), "kv" (keys and values, R =
+        0) or "v" (values into the pages at meta[n:n + count]), validated
+        once and kept."""
+        key = (layer, a, count, kind)
+        plan = self._spill_plans.get(key)
+        if plan is None:
+            G, n = self.config.q_buffer_size, self.num_slots
+            kb = self._qbuf_k[a:a + count, layer] if kind in ("k", "kv") else None
+            vb = self._vbuf[a:a + count, layer, :, :G] if kind in ("kv", "v") else None
+            ids = meta[n:n + count] if kind == "v" else meta[:count]
+            plan = QuantizePlan(self._store, kb, vb, self.boost_idx_uint8[layer] if kb is not None else None, ids,
+                                self.config.sentinel)
+            if len(self._spill_plans) >= 256:
+                self._spill_plans.clear()
+            self._spill_plans[key] = plan
+        return plan
 
     # ------------------------------------------------------------ prefill
     def push_chunk(self, layer_id: int, keys: torch.Tensor, values: torch.Tensor, seq_ids: Sequence[int]) -> None:

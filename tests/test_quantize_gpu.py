@@ -266,7 +266,19 @@ def test_reference_signatures(dev):
     assert np.array_equal(out16.cpu().numpy(), O.dequantize_key(*e, bi.cpu().numpy(), Dk).astype(np.float16))
 
 
-def test_cpu_tensors_are_rejected(dev):
+def test_device_path_rejects_cpu_operands_and_matches_cpu_path(dev):
+    """A device key with a CPU operand is refused by the HIP path (it never
+    computes on the CPU); a CPU key runs the CPU path, whose bytes equal the
+    kernel's."""
     from kitty.kernels import quantize_key_page_torch
+    g = torch.Generator().manual_seed(8)
+    key = (torch.randn(128, 128, generator=g) * 3).half()
+    bi = torch.full((128,), 17, dtype=torch.uint8)
+    bi[torch.randperm(128, generator=g)[:16]] = torch.arange(16, dtype=torch.uint8)
     with pytest.raises(RuntimeError, match="ROCm device"):
-        quantize_key_page_torch(torch.zeros(16, 8, dtype=torch.float16), torch.zeros(16, dtype=torch.uint8), 4, 5)
+        quantize_key_page_torch(key.to(dev), bi, 16, 17)
+    on_cpu = quantize_key_page_torch(key, bi, 16, 17)
+    on_dev = quantize_key_page_torch(key.to(dev), bi.to(dev), 16, 17)
+    assert all(a.device.type == "cpu" for a in on_cpu)
+    for a, b in zip(on_cpu, on_dev):
+        assert torch.equal(a, b.cpu())

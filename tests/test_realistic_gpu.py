@@ -1,7 +1,7 @@
 """Parity on the benchmark's own data: full-size config 3 (x8 outlier key
-channels) and config 5 (x16) pools, built by bench.build_workload from
-seeded fp16 K/V through the HIP quantizer and a shuffled free list, exactly
-as the timed runs build them.
+channels), config 4 (ragged 512-65,536 tokens, 25 % INT4) and config 5 (x16)
+pools, built by bench.build_workload from seeded fp16 K/V through the HIP
+quantizer and a shuffled free list, exactly as the timed runs build them.
 
 * Sampled pool pages, every KV head: the HIP quantizer's bytes against the
   oracle's quantize_key / quantize_value of the same fp16 block, bit for bit
@@ -32,7 +32,8 @@ def _bench():
 GQ16 = dict(B=2, Hq=128, Hkv=8, ctx=32768, boost=0.125, outlier=16.0, seed=16)
 
 
-@pytest.mark.parametrize("name,seqs", [("cfg3", (0, 7, 15)), ("cfg5", (0, 3)), ("gq16", (0, 1))])
+@pytest.mark.parametrize("name,seqs", [("cfg3", (0, 7, 15)), ("cfg5", (0, 3)), ("gq16", (0, 1)),
+                                       ("cfg4", (0, 23, 63))])
 def test_benchmark_workload_parity(dev, name, seqs):
     bench = _bench()
     cfg = GQ16 if name == "gq16" else bench.CONFIGS[name]
@@ -77,3 +78,88 @@ def test_benchmark_workload_parity(dev, name, seqs):
                                 tk[b, :, :t], tv[b, :, :t], w["Hq"], H, D).astype(np.float32)
         err = np.abs(out[b] - ref) - (ATOL + RTOL * np.abs(ref))
         assert (err <= 0).all(), f"{name} b={b}: max excess {err.max():.3g}, max |diff| {np.abs(out[b] - ref).max():.3g}"
+
+
+def test_value_window_layout_at_config3(dev):
+    """The pipeline's production layout at config 3's full size: every
+    sequence's last key page is key-only (P_v = P_k - 1) and its values are
+    the first 128 rows of a 128 + 96-row FP16 value tail (the 128-token
+    value window, pipeline.py:155-168), decoded on the bench's config-3
+    pools and checked, every query head of four sequences, against the
+    oracle's independent-stream decode (kernels/attention.py:136-189 over
+    the assembled key and value streams)."""
+    bench = _bench()
+    cfg = bench.CONFIGS["cfg3"]
+    print("window cfg3: building pools", flush=True)
+    w = bench.build_workload(torch, dev, cfg, 1)
+    from kitty.kernels.ops import DecodePlan
+    B, Hkv, Hq = w["B"], w["Hkv"], w["Hq"]
+    g = torch.Generator(device=dev).manual_seed(333)
+    tv = torch.randn(B, Hkv, 128 + w["n_tail"], D, device=dev, generator=g).half()
+    npk = torch.tensor(w["np_list"], dtype=torch.int32, device=dev)
+    npv = npk - 1
+    tlv = torch.tensor(w["tail_list"], dtype=torch.int32, device=dev) + 128
+    kb, kh, km, vp, vm = w["pools"]
+    plan = DecodePlan(w["q"], w["tables"][0], npk, kb, kh, km, vp, vm, w["bi"], w["sk"], w["sv"],
+                      torch.full((B,), 32, dtype=torch.int32, device=dev), w["tk"], tv,
+                      torch.tensor(w["tail_list"], dtype=torch.int32, device=dev), num_pages_v=npv, tail_len_v=tlv)
+    assert plan.kernel == "mfma"
+    out = plan.run().float().cpu().numpy()
+    assert np.isfinite(out).all()
+    pools = [t.cpu().numpy() for t in w["pools"]]
+    bi = w["bi"].cpu().numpy()
+    bt = w["tables"][0].cpu().numpy()
+    q, sk, sv, tk, tvn = (t.cpu().numpy() for t in (w["q"], w["sk"], w["sv"], w["tk"], tv))
+    print("window cfg3: decoded; checking 4 sequences", flush=True)
+    for b in (0, 5, 10, 15):
+        n, t = w["np_list"][b], w["tail_list"][b]
+        ref = O.paged_attention_kv(q[b], bt[b, :n], bt[b, :n - 1], *pools, bi, w["dk"], sk[b], sv[b], tk[b, :, :t],
+                                   tvn[b, :, :t + 128], Hq, Hkv, D).astype(np.float32)
+        err = np.abs(out[b] - ref) - (ATOL + RTOL * np.abs(ref))
+        assert (err <= 0).all(), f"b={b}: max excess {err.max():.3g}, max |diff| {np.abs(out[b] - ref).max():.3g}"
+
+
+def test_module_decode_at_config3_scale(dev):
+    """KittyPagedAttention at config 3's shape (32 Q / 8 KV heads, d128, S32,
+    G = R = 128, 12.5 % INT4 from x8 outlier channels): three sequences
+    prefilled with push_chunk to 32,767 tokens, then one decode step through
+    the module (the 32,768th token: 255 key pages, 254 value pages, the
+    value window and the key tail), each sequence against the oracle rebuilt
+    from its raw token history (pipeline.py:115-256, attention.py:74-151)."""
+    from histref import oracle_from_history
+    from kitty import KittyAttentionFactory, KittyConfig
+    from kvgen import calibrate_boost_idx, outlier_keys
+    B, H, Hq, ctx = 3, 8, 32, 32768
+    cfg = KittyConfig(num_layers=1, num_kv_heads=H, head_dim=D, q_buffer_size=128, sink_size=32,
+                      local_value_window=128, boost_rate=0.125, max_seq_len=ctx + 256, max_batch_size=B,
+                      device="cuda:0")
+    gen = torch.Generator().manual_seed(31)
+    calib, chans = outlier_keys(gen, (256,), H, D, 16, 8.0)
+    bi = calibrate_boost_idx(calib, cfg.d_boost, cfg.sentinel)
+    layout, pipe, layers = KittyAttentionFactory.from_config(cfg, bi[None], Hq)
+    attn = layers[0]
+    Ks, Vs = [], []
+    for b in range(B):
+        K, _ = outlier_keys(gen, (ctx,), H, D, 16, 8.0, channels=chans)
+        Ks.append(K)
+        Vs.append(torch.randn(ctx, H, D, generator=gen).half())
+    print("module cfg3: prefilling 3 x 32767 tokens", flush=True)
+    kp = torch.stack([K[:ctx - 1].permute(1, 0, 2) for K in Ks]).to(dev)
+    vp = torch.stack([V[:ctx - 1].permute(1, 0, 2) for V in Vs]).to(dev)
+    pipe.push_chunk(0, kp, vp, list(range(B)))
+    del kp, vp
+    q = torch.randn(B, Hq, 1, D, generator=gen).half()
+    k1 = torch.stack([K[ctx - 1:].permute(1, 0, 2) for K in Ks])
+    v1 = torch.stack([V[ctx - 1:].permute(1, 0, 2) for V in Vs])
+    out = attn(q.to(dev), k1.to(dev), v1.to(dev), seq_id=list(range(B)))
+    assert out.shape == (B, Hq, 1, D)
+    assert attn._plans[tuple(range(B))].kernel == "mfma"
+    ctx0 = pipe.get_attention_context(0, 0)
+    assert len(ctx0["page_list"]) == 255 and ctx0["value_pages"] == 254
+    out = out[:, :, 0].float().cpu().numpy()
+    for b in range(B):
+        print(f"module cfg3: oracle for sequence {b}", flush=True)
+        ref = oracle_from_history(Ks[b].numpy(), Vs[b].numpy(), q[b, :, 0].numpy(), 32, 128, bi.numpy(),
+                                  cfg.d_boost, cfg.sentinel, Hq, H, D, R=128).astype(np.float32)
+        err = np.abs(out[b] - ref) - (ATOL + RTOL * np.abs(ref))
+        assert (err <= 0).all(), f"b={b}: max excess {err.max():.3g}, max |diff| {np.abs(out[b] - ref).max():.3g}"
