@@ -170,6 +170,11 @@ int kitty_dequantize_value_page(const kitty_page_store *store, int64_t page, int
  * kitty/kernels/attention.py:148-165).
  * out[b, qh] = softmax(q . K^T * sm_scale) V in fp16; zeros when a sequence
  * has no tokens (:180-182); NaN when its lengths break the rules above.
+ * Range: the MFMA kernel carries 2^-3 q[d] * s_k[d] of every page channel
+ * as fp16 (two rows: product and exact residual), and 2^-1 q[d] * s_k[d] for
+ * a boosted channel's high bits, so |q[d] * s_k[d]| must stay below 2^17
+ * (131,072) on boosted channels and 2^19 on the others; beyond that the
+ * scores of that head are not finite.  The generic kernel computes in fp32.
  *
  * Pools must be the contiguous tensors of PageCentricKVLayoutManager (16-byte
  * aligned bases); page ids are int32 and byte offsets are 64-bit, so a pool

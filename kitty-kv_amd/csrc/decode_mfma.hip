@@ -92,6 +92,10 @@ __device__ __forceinline__ RawCodes raw_codes(i32x2 raw)
 // consumers scale slot a by 2^24 / 4^a.
 constexpr float kSub = 16777216.0f;  // 2^24
 
+// q enters the page path's QK operand times 2^-3 (exact: a power of two),
+// and the scores are multiplied back by 2^3.
+constexpr float kQPre = 0.125f, kQInv = 8.0f;
+
 template <int A>
 __device__ __forceinline__ half8 codes_to_half8(const RawCodes &r)
 {
@@ -674,12 +678,14 @@ __device__ __forceinline__ void qk_setup(WaveState<GQ> &W, const DecodeParams &p
 
     __syncthreads();
 
-    // Static half of the QK A operand: the fp16 q of the lane's 8 channels
+    // Static half of the QK A operand: 2^-3 q (fp16) of the lane's 8 channels
     // of every K-step on the two rows of each head (the product with the key
     // scale and its residual, qk_residual), zero on the other rows.
-    // sm_scale * log2(e) scales the scores, so A stays exact.
+    // 2^3 sm_scale log2(e) scales the scores, so A stays exact; the 2^-3
+    // keeps fp16 products finite up to |q s_k| < 2^19 (2^17 on the high-bit
+    // rows, whose q is also multiplied by 4).
     W.prow = hr;
-    W.qk_c = p.sm_scale * kLog2e;
+    W.qk_c = p.sm_scale * kLog2e * kQInv;
     const bool qk_row = GQ == 16 || (r % ROWS_PER_HEAD) < 2;
     {
         const u32x4 *qraw = su.qraw;
@@ -691,14 +697,15 @@ __device__ __forceinline__ void qk_setup(WaveState<GQ> &W, const DecodeParams &p
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             qh[i] = GQ <= 8 ? q_lds[hr * 128 + W.hch[i]] : *(const _Float16 *)(qrow + W.hch[i]);
+        const half2v pre = {(_Float16)kQPre, (_Float16)kQPre};
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                W.qv[s][j] = qk_row ? qraw[s][j] : 0u;
+                W.qv[s][j] = qk_row ? as_u(as_h2(qraw[s][j]) * pre) : 0u;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float inv = qk_row ? 4.0f : 0.0f;  // high bits weigh 4 (exact in fp16)
+            const float inv = qk_row ? 4.0f * kQPre : 0.0f;  // high bits weigh 4 (exact in fp16)
             const int r0 = 8 * q + 2 * j;
             W.qvh[j] = pack_h2(r0 < Dk ? (float)qh[2 * j] * inv : 0.0f,
                                r0 + 1 < Dk ? (float)qh[2 * j + 1] * inv : 0.0f);
@@ -1047,14 +1054,15 @@ __device__ void fp16_segments(const DecodeParams &p, int b, int kh, int lo, int 
 #pragma unroll
                 for (int j = 0; j < HPL; ++j) {
                     const int ri = j * RSTEP;
-                    const float yk = (GQ == 16 ? Yt[ri] : Yt[ri] + Yt[ri + 1]) * qk_c;
+                    // the page path's scale (its operand carries 2^-3 q)
+                    const float yk = (GQ == 16 ? Yt[ri] : Yt[ri] + Yt[ri + 1]) * W.qk_c;
 #pragma unroll
                     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
                         for (int a = 0; a < 4; ++a)
                             scw[(q * HPL + j) * 128 + 64 * cb + 4 * r + a] =
                                 (GQ == 16 ? Sp[cb][a][ri] : Sp[cb][a][ri] + Sp[cb][a][ri + 1]) *
-                                    (qk_c * (kSub / (float)(1 << (2 * a)))) - yk;
+                                    (W.qk_c * (kSub / (float)(1 << (2 * a)))) - yk;
                 }
                 __syncthreads();  // scores in kst before they are read back
                 page_in_kst = pg;

@@ -241,6 +241,34 @@ def test_invalid_page_id_poisons_output(dev):
     _close(out[0], _oracle_batched(c, Hq, H, D, 0), "b=0")
 
 
+def test_large_query_times_key_scale_stays_finite(dev):
+    """|q[d] s_k[d]| past the fp16 maximum (65,504) but below the documented
+    2^17 / 2^19 bounds: the MFMA kernel's 2^-3 prescaled QK operand stays
+    finite and the output matches the oracle's fp32 scores (here up to
+    |q s| ~ 1.8e5 on the INT2 channels, 3.6e4 on the INT4 ones; the softmax
+    picks one token)."""
+    from kitty.kernels import paged_attention
+    rng = np.random.default_rng(77)
+    H, Hq, D, G, dk, n_pages = 2, 8, 128, 128, 16, 4
+    sentinel = dk + 1
+    c = make_paged_case(rng, H, Hq, D, G, dk, n_pages, 32, 20)
+    for p in c["pages"]:
+        for h in range(H):
+            k = (rng.standard_normal((D, G)) * 600.0).astype(np.float16)
+            c["kb"][p, h], c["kh"][p, h], c["km"][p, h, 0], c["km"][p, h, 1] = O.quantize_key(k, c["bi"][h], dk,
+                                                                                               sentinel)
+    c["q"] = (rng.standard_normal((Hq, D)) * 40.0).astype(np.float16)
+    qs = np.abs(c["q"].astype(np.float64)).max() * np.abs(c["km"][c["pages"], :, 0].astype(np.float64)).max()
+    assert 65504 < qs < 2 ** 19
+    ref = O.paged_attention(c["q"], c["pages"], c["kb"], c["kh"], c["km"], c["vp"], c["vm"], c["bi"], dk,
+                            c["sk"], c["sv"], c["tk"], c["tv"], Hq, H, D)
+    assert np.isfinite(ref.astype(np.float32)).all()
+    q, kb, kh, km, vp, vm, bi, sk, sv, tk, tv = _to(dev, c["q"], c["kb"], c["kh"], c["km"], c["vp"], c["vm"],
+                                                   c["bi"], c["sk"], c["sv"], c["tk"], c["tv"])
+    out = paged_attention(q, [int(p) for p in c["pages"]], kb, kh, km, vp, vm, bi, dk, sk, sv, tk, tv, Hq, H, D)
+    _close(out.cpu().numpy(), ref, "large q s_k")
+
+
 def test_config4_ragged_batch_64bit_offsets(dev):
     """BASELINE config 4 at full size: 64 sequences with seeded ragged
     contexts in [512, 65536], 32 query / 8 KV heads, 25% INT4 channels

@@ -43,8 +43,12 @@ def test_noalloc_matches_workspace_decode(dev, kernel):
         shapes = [(5, 8, 4, 64, 32, 8, [40 + 9 * 32 + 3, 40 + 2 * 32, 40, 40 + 17 * 32 + 31, 40 + 5 * 32 + 1]),
                   (2, 8, 4, 64, 32, 8, [40 + 3 * 32 + 7, 40 + 32])]
     else:
+        # the last two: groups of 20 query heads per KV head, which run as
+        # sub-groups of 16 and 4, each a split + merge through the one scratch
         shapes = [(16, 32, 8, 128, 128, 16, [32 + 40 * 128 + 100] * 12 + [32, 32 + 128, 32 + 7 * 128 + 5, 33]),
-                  (3, 32, 8, 128, 128, 16, [32 + 5 * 128 + 3, 32 + 2 * 128, 32 + 11 * 128 + 127])]
+                  (3, 32, 8, 128, 128, 16, [32 + 5 * 128 + 3, 32 + 2 * 128, 32 + 11 * 128 + 127]),
+                  (2, 40, 2, 128, 128, 16, [32 + 9 * 128 + 40, 32 + 3 * 128 + 5]),
+                  (1, 40, 2, 128, 128, 16, [32 + 2 * 128 + 7])]
     for i, (B, Hq, H, D, G, dk, ctx) in enumerate(shapes):
         print(f"noalloc {kernel} call {i}: B={B} Hq={Hq} H={H} D={D}", flush=True)
         c = _batched_case(dev, 70 + i, B, Hq, H, D, G, dk, ctx, S=32 if D == 128 else 40)
