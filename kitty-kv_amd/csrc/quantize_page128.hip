@@ -49,8 +49,31 @@ constexpr int kLdsBytes = kParOff + 5 * 128 * 4;        // 13,056
 
 __device__ __forceinline__ h2 as_h2(unsigned w) { return __builtin_bit_cast(h2, w); }
 __device__ __forceinline__ unsigned as_u(h2 v) { return __builtin_bit_cast(unsigned, v); }
-__device__ __forceinline__ h2 hmin(h2 a, h2 b) { return __builtin_elementwise_min(a, b); }
-__device__ __forceinline__ h2 hmax(h2 a, h2 b) { return __builtin_elementwise_max(a, b); }
+// Packed fp16 min / max as single instructions.  The builtins' IEEE minnum
+// first quiets each operand that may be a signalling NaN (a v_pk_max_f16
+// x, x per bit-cast operand, about 200 in this kernel); the inputs here are
+// finite fp16, for which the plain instruction gives the same result.
+__device__ __forceinline__ unsigned pk_min(unsigned a, unsigned b)
+{
+    unsigned r;
+    asm("v_pk_min_f16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ unsigned pk_max(unsigned a, unsigned b)
+{
+    unsigned r;
+    asm("v_pk_max_f16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+// min(-a, -b) = -max(a, b), the negation by source modifiers
+__device__ __forceinline__ unsigned pk_min_neg(unsigned a, unsigned b)
+{
+    unsigned r;
+    asm("v_pk_min_f16 %0, %1, %2 neg_lo:[1,1] neg_hi:[1,1]" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ h2 hmin(h2 a, h2 b) { return as_h2(pk_min(as_u(a), as_u(b))); }
+__device__ __forceinline__ h2 hmax(h2 a, h2 b) { return as_h2(pk_max(as_u(a), as_u(b))); }
 
 __device__ __forceinline__ _Float16 chan(const u32x4 &v, int c)
 {
@@ -58,10 +81,12 @@ __device__ __forceinline__ _Float16 chan(const u32x4 &v, int c)
     return __builtin_bit_cast(_Float16, (uint16_t)((c & 1) ? (w >> 16) : (w & 0xffffu)));
 }
 
+// A lane permutation within rows of 16 (every lane has a source, so no old
+// value is needed).
 template <int CTRL>
 __device__ __forceinline__ unsigned dpp(unsigned v)
 {
-    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+    return (unsigned)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
 }
 
 // rint(x / s) of the correctly rounded quotient, without a division per
@@ -161,6 +186,20 @@ __device__ __forceinline__ void magic_exact8(const _Float16 (&x)[8], float s, fl
 __device__ __forceinline__ unsigned code_bits(float t, float mq)
 {
     return __builtin_bit_cast(unsigned, __builtin_amdgcn_fmed3f(t, kC, kC + mq));
+}
+
+// The low bytes of four code words (code_bits: the code is the low byte)
+// as the bytes of one word, a first.
+__device__ __forceinline__ unsigned bytes4(unsigned a, unsigned b, unsigned c, unsigned d)
+{
+    return __builtin_amdgcn_perm(b, a, 0x0c0c0400u) | __builtin_amdgcn_perm(d, c, 0x04000c0cu);
+}
+
+// sum of byte i times 4^i: the 2-bit fields (bits 0-1 of each byte, or bits
+// 2-3 for 4x the field) packed at bits 2i
+__device__ __forceinline__ unsigned dot_pow4(unsigned bytes)
+{
+    return __builtin_amdgcn_udot4(bytes, 0x40100401u, 0u, false);
 }
 
 // 256 bytes of zeros: the rows of a block past `rows_valid` are loaded from
@@ -336,17 +375,20 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
     }
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-        unsigned lo = 0, hi = 0;
+        // the eight 4-bit codes (:95-103) as bytes of two words, tokens 0-3 and 4-7
+        unsigned q[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {                                  // :95-103
-            const unsigned q = code_bits(t[c][k], mq[c]);
-            lo |= (q & 3u) << (2 * k);
-            hi |= ((q >> 2) & 3u) << (2 * k);
-        }
+        for (int k = 0; k < 8; ++k)
+            q[k] = code_bits(t[c][k], mq[c]);
+        const unsigned w0 = bytes4(q[0], q[1], q[2], q[3]), w1 = bytes4(q[4], q[5], q[6], q[7]);
+        // low / high 2 bits of token k's code at bits 2k
+        const unsigned lo = dot_pow4(w0 & 0x03030303u) | (dot_pow4(w1 & 0x03030303u) << 8);
         // token 8tt+k -> byte 2tt + k/4, bits 2(k%4): a 16-bit piece of row d (:108-110)
         *(uint16_t *)(lds + tile_off(8 * cg + c) + 2 * tt) = (uint16_t)lo;
-        if (hr[c] >= 0)                                                // :113-119, OR of the rank's channels
-            atomicOr(high + hr[c] * 8 + (tt >> 1), hi << (16 * (tt & 1)));
+        if (hr[c] >= 0) {                                              // :113-119, OR of the rank's channels
+            const unsigned hi4 = dot_pow4(w0 & 0x0c0c0c0cu) | (dot_pow4(w1 & 0x0c0c0c0cu) << 8);
+            atomicOr(high + hr[c] * 8 + (tt >> 1), (hi4 >> 2) << (16 * (tt & 1)));
+        }
     }
     __syncthreads();
     if (!ok)
@@ -377,35 +419,40 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
     bool ok;
     const int64_t page = dest_page(L, o, i, ok);
 
-    // (min, -max) of each token over the thread's 8 channels, packed in fp16,
-    // then over the 16 lanes of the DPP row (:63-64)
+    // (min, -max) of each token over the thread's 8 channels, packed in fp16
+    // (:63-64): min over the four channel pairs, the same over the negated
+    // pairs, then the two halves of each against each other
     unsigned mm[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        const h2 a = hmin(hmin(as_h2(r[k][0]), as_h2(r[k][1])), hmin(as_h2(r[k][2]), as_h2(r[k][3])));
-        const h2 b = hmax(hmax(as_h2(r[k][0]), as_h2(r[k][1])), hmax(as_h2(r[k][2]), as_h2(r[k][3])));
-        // (a.x, -b.x) and (a.y, -b.y): byte-select, then flip the sign of the high half
-        const unsigned lo = __builtin_amdgcn_perm(as_u(b), as_u(a), 0x05040100u) ^ 0x80000000u;
-        const unsigned hi = __builtin_amdgcn_perm(as_u(b), as_u(a), 0x07060302u) ^ 0x80000000u;
-        unsigned v = as_u(hmin(as_h2(lo), as_h2(hi)));
-        v = as_u(hmin(as_h2(v), as_h2(dpp<0x128>(v))));
-        v = as_u(hmin(as_h2(v), as_h2(dpp<0x124>(v))));
-        v = as_u(hmin(as_h2(v), as_h2(dpp<0x122>(v))));
-        mm[k] = as_u(hmin(as_h2(v), as_h2(dpp<0x121>(v))));
+        const unsigned a = pk_min(pk_min(r[k][0], r[k][1]), pk_min(r[k][2], r[k][3]));
+        const unsigned b = pk_min(pk_min_neg(r[k][0], r[k][1]), pk_min_neg(r[k][2], r[k][3]));
+        mm[k] = pk_min(__builtin_amdgcn_perm(b, a, 0x05040100u), __builtin_amdgcn_perm(b, a, 0x07060302u));
     }
-
-    // lane k < 8 of each row: parameters of token 8tt + k
-    float *ps = (float *)(lds + kParOff), *prs = ps + 128, *pz = ps + 256;
-    if (cg < 8) {
-        unsigned v = mm[0];
+    // ... then over the 16 lanes of the DPP row, as a reduce-scatter: each
+    // step pairs lane l with a partner (l ^ 15, l ^ 7, l ^ 2, l ^ 1), keeps
+    // half of its tokens and takes the partner's partials of that half.  The
+    // partners' XOR masks span all 16 lanes, so lane l ends with token
+    // (l % 16) / 2 reduced over the whole row (lanes 2j and 2j + 1 alike).
+    const bool b3 = cg & 8, b2 = cg & 4, b1 = cg & 2;
+    unsigned w[4], x[2];
 #pragma unroll
-        for (int k = 1; k < 8; ++k)
-            v = cg == k ? mm[k] : v;
+    for (int j = 0; j < 4; ++j)   // row_mirror: l <-> 15 - l
+        w[j] = pk_min(b3 ? mm[j + 4] : mm[j], dpp<0x140>(b3 ? mm[j] : mm[j + 4]));
+#pragma unroll
+    for (int j = 0; j < 2; ++j)   // row_half_mirror: l <-> l ^ 7
+        x[j] = pk_min(b2 ? w[j + 2] : w[j], dpp<0x141>(b2 ? w[j] : w[j + 2]));
+    unsigned v = pk_min(b1 ? x[1] : x[0], dpp<0x4E>(b1 ? x[0] : x[1]));   // quad_perm [2,3,0,1]
+    v = pk_min(v, dpp<0xB1>(v));                                           // quad_perm [1,0,3,2]
+
+    // even lanes of each row: parameters of token 8tt + cg / 2
+    float *ps = (float *)(lds + kParOff), *prs = ps + 128, *pz = ps + 256;
+    if ((cg & 1) == 0) {
         const float mn = h2f((uint16_t)(v & 0xffffu)), mx = -h2f((uint16_t)(v >> 16));
         const float s = range_of(mn, mx) / 3.0f;                       // :65-67
         const float rs = __builtin_amdgcn_rcpf(s);
         const float z = zp_clamp(rint_quot(-mn, s, rs), 3.0f);         // :69-73
-        const int t = 8 * tt + cg;
+        const int t = 8 * tt + (cg >> 1);
         ps[t] = s;
         prs[t] = rs;
         pz[t] = z;
@@ -436,13 +483,12 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        // :74-88, channel 4j+i at byte j bits 2i; a code is at most 3, and the
-        // words' constant high bits land at bit 24 and above: the low 16 bits
-        // are the packed codes
-        unsigned bits = code_bits(t[k][0], 3.0f);
+        // :74-88, channel 4j+i at byte j bits 2i (codes are at most 3)
+        unsigned q[8];
 #pragma unroll
-        for (int c = 1; c < 8; ++c)
-            bits |= code_bits(t[k][c], 3.0f) << (2 * c);
+        for (int c = 0; c < 8; ++c)
+            q[c] = code_bits(t[k][c], 3.0f);
+        const unsigned bits = dot_pow4(bytes4(q[0], q[1], q[2], q[3])) | (dot_pow4(bytes4(q[4], q[5], q[6], q[7])) << 8);
         *(uint16_t *)(lds + tile_off(8 * tt + k) + 2 * cg) = (uint16_t)bits;
     }
     __syncthreads();
