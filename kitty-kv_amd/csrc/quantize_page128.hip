@@ -1,21 +1,24 @@
 // Batch quantise + pack for the production page shape D = G = 128 on gfx950.
 //
-// One 256-thread workgroup per (block, role): role 0 packs the key block per
+// One 512-thread workgroup per (block, role): role 0 packs the key block per
 // channel, role 1 the value block per token.  Thread (tt, cg), tt = 4 * wave
-// + lane / 16 and cg = lane % 16, loads tokens 8tt..8tt+7 x channels
-// 8cg..8cg+7 of the fp16 block with eight 16-byte loads, all issued before any
+// + lane / 16 and cg = lane % 16, loads tokens 4tt..4tt+3 x channels
+// 8cg..8cg+7 of the fp16 block with four 16-byte loads, all issued before any
 // arithmetic (32 KB in flight per workgroup, one 256-byte token row per 16
-// lanes).
+// lanes).  Eight waves per block: the code phase after the loads land is
+// bound by the latency of dependent VALU instructions, which more waves per
+// SIMD hide (config 2's 512 workgroups give four per SIMD).
 //
-// Keys: packed-fp16 min / max over the thread's 8 tokens, then across lanes
-// 16 and 32 apart, then across the 4 waves in LDS; one thread per channel
+// Keys: packed-fp16 min / max over the thread's 4 tokens, then across lanes
+// 16 and 32 apart, then across the 8 waves in LDS; one thread per channel
 // turns (min, max) into (s, 1/s, z) and the stored fp16 scale / zero point.
 // Values: packed-fp16 (min, -max) over the thread's 8 channels, then across
-// the 16 lanes of a DPP row; lane k of the row computes the parameters of
-// the row's token k.  Parameters go through LDS to the threads that code the
-// elements.  Each thread packs its 8 x 8 codes into 16-bit pieces of the
-// packed rows, the page is assembled in LDS, and the workgroup writes the
-// 4 KB code region with one 16-byte store per thread.
+// the 16 lanes of a DPP row, as a reduce-scatter that leaves each token's
+// range with four lanes, one of which computes its parameters.  Parameters
+// go through LDS to the threads that code the elements.  Each thread packs
+// its 8 x 4 codes into 8-bit (keys) or 16-bit (values) pieces of the packed
+// rows, the page is assembled in LDS, and the workgroup writes the 4 KB code
+// region with one 16-byte store per thread of its first half.
 //
 // The block's loads do not wait for anything: rows past the valid ones read
 // a zero row instead of branching, and the destination page id is looked up
@@ -24,7 +27,7 @@
 // Arithmetic is that of quantize.h (bit-exact with the reference).  The
 // zero points use the multiply-by-reciprocal of rint_quot below, which
 // returns the same integer as rint of the correctly rounded quotient; the
-// codes use the same argument in the fused form of magic_fast8x8, eight
+// codes use the same argument in the fused form of magic_fast, eight
 // elements at a time, with the code left in the low bits of a float.
 #include "quantize.h"
 
@@ -35,7 +38,9 @@ namespace kitty {
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
+constexpr int kTok = 4;                                  // tokens per thread
 
 // LDS layout (bytes).  The code tile holds 128 rows x 32 B with 16 B of
 // padding after every 8 rows, so the rows a wave writes together (8 apart)
@@ -43,9 +48,9 @@ constexpr int kThreads = 256;
 __device__ __forceinline__ int tile_off(int row) { return row * 32 + (row >> 3) * 16; }
 constexpr int kTileBytes = 128 * 32 + 16 * 16;          // 4,352
 constexpr int kHighOff = kTileBytes;                    // key high rows, <= 128 x 32 B
-constexpr int kRedOff = kHighOff + 128 * 32;            // key partial min / max: 2 x 4 waves x 128 fp16
-constexpr int kParOff = kRedOff + 2 * 4 * 128 * 2;      // parameters: s, 1/s, z, mq, high row: 5 x 128 x 4 B
-constexpr int kLdsBytes = kParOff + 5 * 128 * 4;        // 13,056
+constexpr int kRedOff = kHighOff + 128 * 32;            // key partial min / max: 2 x 8 waves x 128 fp16
+constexpr int kParOff = kRedOff + 2 * kWaves * 128 * 2; // parameters: s, 1/s, z, mq, high row: 5 x 128 x 4 B
+constexpr int kLdsBytes = kParOff + 5 * 128 * 4;        // 15,104
 
 __device__ __forceinline__ h2 as_h2(unsigned w) { return __builtin_bit_cast(h2, w); }
 __device__ __forceinline__ unsigned as_u(h2 v) { return __builtin_bit_cast(unsigned, v); }
@@ -125,42 +130,42 @@ __device__ __forceinline__ float rint_quot(float x, float s, float rs)
 // near a half-integer recomputes all eight from the correctly rounded
 // quotient.  The fp16 operands are read in place (v_fma_mix_f32).
 //
-// The kernels run the fast step of all eight groups of a thread first and
-// the (rarely taken) exact recomputations after.
+// The kernels run the fast step of all groups of a thread first and the
+// (rarely taken) exact recomputations after.
 constexpr float kC = 0x1p23f;
 constexpr float kNearHalf = 0.5f - 0x1p-14f;
 
-// Fast step for a thread's eight groups of eight, x(g, e) the fp16 element:
-// t[g][e] = fma(x, rs[g], cz[g]) (cz = kC + z) and dev[g] = the group's
-// largest |p - rint(p)|.  The work runs in phases (every t, every t - cz,
+// Fast step for a thread's NG groups of eight, x(g, e) the fp16 element with
+// parameters rs(g, e), cz(g, e): t[g][e] = fma(x, rs, cz) (cz = kC + z) and
+// dev[g] = the group's largest |p - rint(p)|.  The work runs in phases (every t, every t - cz,
 // every e, the maxima) with scheduling barriers between them, four groups at
 // a time: a phase is 32 independent operations, so no result is read by the
 // instruction after the one that wrote it (a v_fma_mix_f32 result read at
 // once costs a wait state) and the groups' latencies overlap.
-template <typename X>
-__device__ __forceinline__ void magic_fast8x8(X x, const float (&rs)[8], const float (&cz)[8], float (&t)[8][8],
-                                              float (&dev)[8])
+template <int NG, typename X, typename RS, typename CZ>
+__device__ __forceinline__ void magic_fast(X x, RS rs, CZ cz, float (&t)[NG][8], float (&dev)[NG])
 {
+    static_assert(NG % 4 == 0, "groups come in fours");
 #pragma unroll
-    for (int h = 0; h < 8; h += 4) {
+    for (int h = 0; h < NG; h += 4) {
         float n[4][8];
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                t[h + g][e] = __builtin_fmaf((float)x(h + g, e), rs[h + g], cz[h + g]);
+                t[h + g][e] = __builtin_fmaf((float)x(h + g, e), rs(h + g, e), cz(h + g, e));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                n[g][e] = t[h + g][e] - cz[h + g];
+                n[g][e] = t[h + g][e] - cz(h + g, e);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                n[g][e] = __builtin_fmaf((float)x(h + g, e), rs[h + g], -n[g][e]);
+                n[g][e] = __builtin_fmaf((float)x(h + g, e), rs(h + g, e), -n[g][e]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -181,7 +186,7 @@ __device__ __forceinline__ void magic_exact8(const _Float16 (&x)[8], float s, fl
         t[e] = __builtin_rintf((float)x[e] / s) + cz;  // cz exact: z is an integer in [0, 15]
 }
 
-// The clamped code of t from magic_fast8x8 / magic_exact8 as the low bits of a word:
+// The clamped code of t from magic_fast / magic_exact8 as the low bits of a word:
 // kC + clamp(t - kC, 0, mq) has the bit pattern 0x4B000000 | code.
 __device__ __forceinline__ unsigned code_bits(float t, float mq)
 {
@@ -206,41 +211,45 @@ __device__ __forceinline__ unsigned dot_pow4(unsigned bytes)
 // here (16 bytes per lane of a token row; never written).
 __device__ u32x4 kZeroRow[16];
 
-// Rows t0..t0+7 of a token-major fp16 block, channels 8cg..8cg+7 (`src`
+// Rows t0..t0+3 of a token-major fp16 block, channels 8cg..8cg+7 (`src`
 // already points at channel 8cg); rows at or past `rows_valid` read as zeros
 // (the reference's zero-padded value rows).  Every load is issued
-// unconditionally, the eight together: a row past the block reads the zero
+// unconditionally, the four together: a row past the block reads the zero
 // row instead, so no branch (and no wait at its join) separates the loads.
 // The source is read once: the loads are non-temporal.
 __device__ __forceinline__ void load_rows(const uint16_t *src, int64_t s_tok, int t0, int rows_valid, int cg,
-                                          u32x4 (&r)[8])
+                                          u32x4 (&r)[kTok])
 {
     const uint16_t *base = src + (int64_t)t0 * s_tok;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kTok; ++k) {
         const u32x4 *ptr = t0 + k < rows_valid ? (const u32x4 *)(base + k * s_tok) : &kZeroRow[cg];
         r[k] = __builtin_nontemporal_load(ptr);
     }
 }
 
-// Code region of the page (128 rows x 32 B, contiguous): one 16-byte store per thread.
+// Code region of the page (128 rows x 32 B, contiguous): one 16-byte store
+// per thread of the first 256.
 __device__ __forceinline__ void store_tile(uint8_t *dst, const unsigned char *tile, int tid)
 {
-    *(u32x4 *)(dst + 16 * tid) = *(const u32x4 *)(tile + tile_off(tid >> 1) + 16 * (tid & 1));
+    if (tid < 256)
+        *(u32x4 *)(dst + 16 * tid) = *(const u32x4 *)(tile + tile_off(tid >> 1) + 16 * (tid & 1));
 }
 
-// Eight consecutive 32-bit LDS words.  (Each element is copied to a scalar
-// before the bit cast: clang's __builtin_bit_cast of an ext_vector element
-// expression reads element 0.)
-template <typename T>
-__device__ __forceinline__ void read8(const unsigned char *lds, int off, T (&v)[8])
+// N (4 or 8) consecutive 32-bit LDS words.  (Each element is copied to a
+// scalar before the bit cast: clang's __builtin_bit_cast of an ext_vector
+// element expression reads element 0.)
+template <int N, typename T>
+__device__ __forceinline__ void readn(const unsigned char *lds, int off, T (&v)[N])
 {
-    const u32x4 a = *(const u32x4 *)(lds + off), b = *(const u32x4 *)(lds + off + 16);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const unsigned wa = a[c], wb = b[c];
-        v[c] = __builtin_bit_cast(T, wa);
-        v[c + 4] = __builtin_bit_cast(T, wb);
+    for (int h = 0; h < N; h += 4) {
+        const u32x4 a = *(const u32x4 *)(lds + off + 4 * h);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const unsigned w = a[c];
+            v[h + c] = __builtin_bit_cast(T, w);
+        }
     }
 }
 
@@ -257,17 +266,18 @@ __device__ __forceinline__ int64_t dest_page(const QuantLaunch &L, int o, int i,
 // ------------------------------------------------------------------- keys
 // quantize_key.py:69-124: per channel over the 128 tokens.
 // Channel-major key blocks (token stride 1, the reference signature's (D, G)
-// key): the thread's tile comes as eight 16-byte loads of 8 tokens of one
+// key): the thread's tile comes as eight 8-byte loads of 4 tokens of one
 // channel each and is transposed in registers to token rows (one v_perm_b32
 // per output word: the same 16-bit half of two channels' words).
-__device__ __forceinline__ void load_tile_channel_major(const uint16_t *src, int64_t s_chan, u32x4 (&r)[8])
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void load_tile_channel_major(const uint16_t *src, int64_t s_chan, u32x4 (&r)[kTok])
 {
-    u32x4 c[8];
+    u32x2 c[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-        c[j] = __builtin_nontemporal_load((const u32x4 *)(src + j * s_chan));
+        c[j] = __builtin_nontemporal_load((const u32x2 *)(src + j * s_chan));
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < kTok; ++k)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             r[k][j] = __builtin_amdgcn_perm(c[2 * j + 1][k >> 1], c[2 * j][k >> 1], (k & 1) ? 0x07060302u : 0x05040100u);
@@ -282,12 +292,12 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
     const int cg = lane & 15, tt = wave * 4 + (lane >> 4);
     const int Dk = st.d_boost;
 
-    u32x4 r[8];
+    u32x4 r[kTok];
     if constexpr (CHAN_MAJOR)
-        load_tile_channel_major(qb.key + outer_offset(qb, o, qb.key_s_seq, qb.key_s_outer) + i * qb.key_s_inner + 8 * cg * qb.key_s_chan + 8 * tt,
+        load_tile_channel_major(qb.key + outer_offset(qb, o, qb.key_s_seq, qb.key_s_outer) + i * qb.key_s_inner + 8 * cg * qb.key_s_chan + kTok * tt,
                                 qb.key_s_chan, r);
     else
-        load_rows(qb.key + outer_offset(qb, o, qb.key_s_seq, qb.key_s_outer) + i * qb.key_s_inner + 8 * cg, qb.key_s_tok, 8 * tt, 128, cg, r);
+        load_rows(qb.key + outer_offset(qb, o, qb.key_s_seq, qb.key_s_outer) + i * qb.key_s_inner + 8 * cg, qb.key_s_tok, kTok * tt, 128, cg, r);
     // boost rank of channel tid (threads 128.. load a copy and ignore it)
     const int b = qb.boost_idx[o * qb.boost_s_outer + i * qb.boost_s_inner + (tid & 127)];
     bool ok;
@@ -303,7 +313,7 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
     for (int j = 0; j < 4; ++j)
         mn[j] = mx[j] = as_h2(r[0][j]);
 #pragma unroll
-    for (int k = 1; k < 8; ++k)
+    for (int k = 1; k < kTok; ++k)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             mn[j] = hmin(mn[j], as_h2(r[k][j]));
@@ -318,7 +328,7 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
     }
     if (lane < 16) {  // the wave's partial for channels 8cg..8cg+7
         *(u32x4 *)(lds + kRedOff + wave * 256 + cg * 16) = u32x4{as_u(mn[0]), as_u(mn[1]), as_u(mn[2]), as_u(mn[3])};
-        *(u32x4 *)(lds + kRedOff + 1024 + wave * 256 + cg * 16) =
+        *(u32x4 *)(lds + kRedOff + kWaves * 256 + wave * 256 + cg * 16) =
             u32x4{as_u(mx[0]), as_u(mx[1]), as_u(mx[2]), as_u(mx[3])};
     }
     __syncthreads();
@@ -330,10 +340,10 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
     // registers get reused, and reuse waits for every outstanding store)
     uint16_t meta_s = 0, meta_z = 0;
     if (tid < 128) {  // channel d = tid
-        const uint16_t *rmn = (const uint16_t *)(lds + kRedOff), *rmx = rmn + 512;
+        const uint16_t *rmn = (const uint16_t *)(lds + kRedOff), *rmx = rmn + kWaves * 128;
         float cmn = h2f(rmn[tid]), cmx = h2f(rmx[tid]);
 #pragma unroll
-        for (int w2 = 1; w2 < 4; ++w2) {
+        for (int w2 = 1; w2 < kWaves; ++w2) {
             cmn = __builtin_fminf(cmn, h2f(rmn[w2 * 128 + tid]));
             cmx = __builtin_fmaxf(cmx, h2f(rmx[w2 * 128 + tid]));
         }
@@ -353,42 +363,40 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
 
     float s[8], rs[8], z[8], mq[8];
     int hr[8];
-    read8(lds, kParOff + 32 * cg, s);
-    read8(lds, kParOff + 512 + 32 * cg, rs);
-    read8(lds, kParOff + 1024 + 32 * cg, z);
-    read8(lds, kParOff + 1536 + 32 * cg, mq);
-    read8(lds, kParOff + 2048 + 32 * cg, hr);
-    float t[8][8], dev[8], cz[8];
+    readn<8>(lds, kParOff + 32 * cg, s);
+    readn<8>(lds, kParOff + 512 + 32 * cg, rs);
+    readn<8>(lds, kParOff + 1024 + 32 * cg, z);
+    readn<8>(lds, kParOff + 1536 + 32 * cg, mq);
+    readn<8>(lds, kParOff + 2048 + 32 * cg, hr);
+    // groups of eight elements: t[g][e] is channel 2g + e / 4, token e % 4
+    // (two channels share a group's near-half check, not their parameters)
+    float t[4][8], dev[4], cz[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c)
         cz[c] = kC + z[c];
-    magic_fast8x8([&](int c, int k) { return chan(r[k], c); }, rs, cz, t, dev);
+    magic_fast<4>([&](int g, int e) { return chan(r[e & 3], 2 * g + (e >> 2)); },
+                  [&](int g, int e) { return rs[2 * g + (e >> 2)]; },
+                  [&](int g, int e) { return cz[2 * g + (e >> 2)]; }, t, dev);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        if (__builtin_expect(dev[c] > kNearHalf, 0)) {
-            _Float16 x[8];
+    for (int g = 0; g < 4; ++g) {
+        if (__builtin_expect(dev[g] > kNearHalf, 0)) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                x[k] = chan(r[k], c);
-            magic_exact8(x, s[c], cz[c], t[c]);
+            for (int e = 0; e < 8; ++e) {
+                const int c = 2 * g + (e >> 2), k = e & 3;
+                t[g][e] = __builtin_rintf((float)chan(r[k], c) / s[c]) + cz[c];
+            }
         }
     }
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-        // the eight 4-bit codes (:95-103) as bytes of two words, tokens 0-3 and 4-7
-        unsigned q[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-            q[k] = code_bits(t[c][k], mq[c]);
-        const unsigned w0 = bytes4(q[0], q[1], q[2], q[3]), w1 = bytes4(q[4], q[5], q[6], q[7]);
-        // low / high 2 bits of token k's code at bits 2k
-        const unsigned lo = dot_pow4(w0 & 0x03030303u) | (dot_pow4(w1 & 0x03030303u) << 8);
-        // token 8tt+k -> byte 2tt + k/4, bits 2(k%4): a 16-bit piece of row d (:108-110)
-        *(uint16_t *)(lds + tile_off(8 * cg + c) + 2 * tt) = (uint16_t)lo;
-        if (hr[c] >= 0) {                                              // :113-119, OR of the rank's channels
-            const unsigned hi4 = dot_pow4(w0 & 0x0c0c0c0cu) | (dot_pow4(w1 & 0x0c0c0c0cu) << 8);
-            atomicOr(high + hr[c] * 8 + (tt >> 1), (hi4 >> 2) << (16 * (tt & 1)));
-        }
+        // the four 4-bit codes (:95-103) as the bytes of a word
+        const int g = c >> 1, e0 = 4 * (c & 1);
+        const unsigned w = bytes4(code_bits(t[g][e0], mq[c]), code_bits(t[g][e0 + 1], mq[c]),
+                                  code_bits(t[g][e0 + 2], mq[c]), code_bits(t[g][e0 + 3], mq[c]));
+        // token 4tt+k -> byte tt, bits 2k: an 8-bit piece of row d (:108-110)
+        lds[tile_off(8 * cg + c) + tt] = (unsigned char)dot_pow4(w & 0x03030303u);
+        if (hr[c] >= 0)                                                // :113-119, OR of the rank's channels
+            atomicOr(high + hr[c] * 8 + (tt >> 2), (dot_pow4(w & 0x0c0c0c0cu) >> 2) << (8 * (tt & 3)));
     }
     __syncthreads();
     if (!ok)
@@ -413,8 +421,8 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cg = lane & 15, tt = wave * 4 + (lane >> 4);
 
-    u32x4 r[8];
-    load_rows(qb.value + outer_offset(qb, o, qb.value_s_seq, qb.value_s_outer) + i * qb.value_s_inner + 8 * cg, qb.value_s_tok, 8 * tt,
+    u32x4 r[kTok];
+    load_rows(qb.value + outer_offset(qb, o, qb.value_s_seq, qb.value_s_outer) + i * qb.value_s_inner + 8 * cg, qb.value_s_tok, kTok * tt,
               qb.value_rows, cg, r);
     bool ok;
     const int64_t page = dest_page(L, o, i, ok);
@@ -422,37 +430,36 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
     // (min, -max) of each token over the thread's 8 channels, packed in fp16
     // (:63-64): min over the four channel pairs, the same over the negated
     // pairs, then the two halves of each against each other
-    unsigned mm[8];
+    unsigned mm[kTok];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kTok; ++k) {
         const unsigned a = pk_min(pk_min(r[k][0], r[k][1]), pk_min(r[k][2], r[k][3]));
         const unsigned b = pk_min(pk_min_neg(r[k][0], r[k][1]), pk_min_neg(r[k][2], r[k][3]));
         mm[k] = pk_min(__builtin_amdgcn_perm(b, a, 0x05040100u), __builtin_amdgcn_perm(b, a, 0x07060302u));
     }
-    // ... then over the 16 lanes of the DPP row, as a reduce-scatter: each
-    // step pairs lane l with a partner (l ^ 15, l ^ 7, l ^ 2, l ^ 1), keeps
-    // half of its tokens and takes the partner's partials of that half.  The
-    // partners' XOR masks span all 16 lanes, so lane l ends with token
-    // (l % 16) / 2 reduced over the whole row (lanes 2j and 2j + 1 alike).
-    const bool b3 = cg & 8, b2 = cg & 4, b1 = cg & 2;
-    unsigned w[4], x[2];
+    // ... then over the 16 lanes of the DPP row, as a reduce-scatter: the
+    // first two steps pair lane l with a partner (l ^ 15, then l ^ 7), keep
+    // half of its tokens and take the partner's partials of that half; the
+    // last two (l ^ 2, l ^ 1) combine the partner's partial of the same
+    // token.  The XOR masks span all 16 lanes, so lane l ends with token
+    // (l % 16) / 4 reduced over the whole row (lanes 4j .. 4j + 3 alike).
+    const bool b3 = cg & 8, b2 = cg & 4;
+    unsigned w[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)   // row_mirror: l <-> 15 - l
-        w[j] = pk_min(b3 ? mm[j + 4] : mm[j], dpp<0x140>(b3 ? mm[j] : mm[j + 4]));
-#pragma unroll
-    for (int j = 0; j < 2; ++j)   // row_half_mirror: l <-> l ^ 7
-        x[j] = pk_min(b2 ? w[j + 2] : w[j], dpp<0x141>(b2 ? w[j] : w[j + 2]));
-    unsigned v = pk_min(b1 ? x[1] : x[0], dpp<0x4E>(b1 ? x[0] : x[1]));   // quad_perm [2,3,0,1]
+    for (int j = 0; j < 2; ++j)   // row_mirror: l <-> 15 - l
+        w[j] = pk_min(b3 ? mm[j + 2] : mm[j], dpp<0x140>(b3 ? mm[j] : mm[j + 2]));
+    unsigned v = pk_min(b2 ? w[1] : w[0], dpp<0x141>(b2 ? w[0] : w[1]));   // row_half_mirror: l <-> l ^ 7
+    v = pk_min(v, dpp<0x4E>(v));                                           // quad_perm [2,3,0,1]
     v = pk_min(v, dpp<0xB1>(v));                                           // quad_perm [1,0,3,2]
 
-    // even lanes of each row: parameters of token 8tt + cg / 2
+    // lanes 4j of each row: parameters of token 4tt + j
     float *ps = (float *)(lds + kParOff), *prs = ps + 128, *pz = ps + 256;
-    if ((cg & 1) == 0) {
+    if ((cg & 3) == 0) {
         const float mn = h2f((uint16_t)(v & 0xffffu)), mx = -h2f((uint16_t)(v >> 16));
         const float s = range_of(mn, mx) / 3.0f;                       // :65-67
         const float rs = __builtin_amdgcn_rcpf(s);
         const float z = zp_clamp(rint_quot(-mn, s, rs), 3.0f);         // :69-73
-        const int t = 8 * tt + (cg >> 1);
+        const int t = kTok * tt + (cg >> 2);
         ps[t] = s;
         prs[t] = rs;
         pz[t] = z;
@@ -462,17 +469,18 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
     }
     __syncthreads();
 
-    float s[8], rs[8], z[8];
-    read8(lds, kParOff + 32 * tt, s);
-    read8(lds, kParOff + 512 + 32 * tt, rs);
-    read8(lds, kParOff + 1024 + 32 * tt, z);
-    float t[8][8], dev[8], cz[8];
+    float s[kTok], rs[kTok], z[kTok];
+    readn<kTok>(lds, kParOff + 4 * kTok * tt, s);
+    readn<kTok>(lds, kParOff + 512 + 4 * kTok * tt, rs);
+    readn<kTok>(lds, kParOff + 1024 + 4 * kTok * tt, z);
+    float t[kTok][8], dev[kTok], cz[kTok];
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < kTok; ++k)
         cz[k] = kC + z[k];
-    magic_fast8x8([&](int k, int c) { return chan(r[k], c); }, rs, cz, t, dev);
+    magic_fast<kTok>([&](int k, int c) { return chan(r[k], c); }, [&](int k, int) { return rs[k]; },
+                     [&](int k, int) { return cz[k]; }, t, dev);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kTok; ++k) {
         if (__builtin_expect(dev[k] > kNearHalf, 0)) {
             _Float16 x[8];
 #pragma unroll
@@ -482,14 +490,14 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
         }
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kTok; ++k) {
         // :74-88, channel 4j+i at byte j bits 2i (codes are at most 3)
         unsigned q[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c)
             q[c] = code_bits(t[k][c], 3.0f);
         const unsigned bits = dot_pow4(bytes4(q[0], q[1], q[2], q[3])) | (dot_pow4(bytes4(q[4], q[5], q[6], q[7])) << 8);
-        *(uint16_t *)(lds + tile_off(8 * tt + k) + 2 * cg) = (uint16_t)bits;
+        *(uint16_t *)(lds + tile_off(kTok * tt + k) + 2 * cg) = (uint16_t)bits;
     }
     __syncthreads();
     if (ok)
