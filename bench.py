@@ -436,14 +436,21 @@ def module_leg(torch, dev, cfg_name: str = "cfg3", cycles: int = 2, event_cycles
     n_ev = event_cycles * G
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev + 1)]
     torch.cuda.synchronize()
+    slot0 = pipe.slot(seq_ids[0])
+    spills = []
     ev[0].record()
     for i in range(n_ev):
+        # the sequences run in lockstep: this step spills them all when the
+        # first one's key or value buffer is one token from full
+        spills.append(int(pipe._qlen[slot0, 0]) + 1 == G or int(pipe._vlen[slot0, 0]) + 1 == pipe.value_capacity)
         attn(qs[i % steps], ks[i % steps], vs[i % steps], seq_id=seq_ids)
         ev[i + 1].record()
     torch.cuda.synchronize()
     per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(n_ev)]
-    med = statistics.median(per)
-    # the sequences run in lockstep: one step of each cycle spills them all
+    assert sum(spills) >= event_cycles, "a spill step in every cycle"
+    med = statistics.median(p for p, sp in zip(per, spills) if not sp)
+    spill_us = statistics.median(p for p, sp in zip(per, spills) if sp)
+    # the largest step of each cycle, spill or not (host noise: collector pauses, scheduling)
     worst = statistics.median(max(per[j * G:(j + 1) * G]) for j in range(event_cycles))
     plan = attn._plans.get(tuple(range(B)))
     assert plan is not None, "the decode plan is cached across steps"
@@ -453,20 +460,28 @@ def module_leg(torch, dev, cfg_name: str = "cfg3", cycles: int = 2, event_cycles
                         f"contexts {ctx - G + 1}..{ctx + (cycles - 1) * G}, S{S} G{G} R128 "
                         f"{int(c['boost'] * 1000) / 10}% INT4 keys",
             "us_per_step": round(wall_us, 2), "us_per_step_events": round(event_us, 2), "steps": n_t,
-            "step_us_median": round(med, 2), "spill_step_us": round(worst, 2),
-            "spill_step_extra_us": round(worst - med, 2), "spill_steps_timed": event_cycles,
-            "note": "each step: append of all B tokens, key/value spills every G steps (one key-only and one "
-                    "value-only batch-quantize launch over B*Hkv blocks plus the value-buffer shift), decode "
-                    "with independent key/value streams (page-pair split kernel, key-only pages in its FP16 "
-                    "segments) and merge; host clock over the timed steps includes the Python module overhead"}
+            "step_us_median": round(med, 2), "spill_step_us": round(spill_us, 2),
+            "spill_step_extra_us": round(spill_us - med, 2), "spill_steps_timed": sum(spills),
+            "cycle_max_step_us": round(worst, 2),
+            "note": "each step: append of all B tokens; every G steps a spill (one kitty_store_i32 launch for "
+                    "the new pages' ids, block-table entries and counters, then one batch-quantize launch of "
+                    "B*Hkv key and B*Hkv value blocks whose value blocks also shift the 128-token value window); "
+                    "decode with independent key/value streams (page-pair split kernel, key-only pages in its "
+                    "FP16 segments) and merge.  step_us_median: median event time of the steps without a spill; "
+                    "spill_step_us: median of the spill steps; cycle_max_step_us: median over cycles of each "
+                    "cycle's largest step, spill or not (host noise included); host clock over the timed steps "
+                    "includes the Python module overhead"}
 
 
 def spill_latency(torch, dev, B: int = 16, Hkv: int = 8, dk: int = 16, reps: int = 64) -> dict:
     """The pipeline's spill launches at their production shape: one
     kitty_quantize_kv_blocks launch over the B * Hkv (G x D) blocks of one
-    layer (config-3 batch), key and value together (R = 0), key only and
-    value only (a 128-token value window), each timed as bursts of `reps`
-    back-to-back launches over 8 rotating input / page sets."""
+    layer (config-3 batch): key and value into the same pages (R = 0), key
+    only, value only, and the spill of the 128-token value window as the
+    pipeline makes it (keys into new pages, values into their own pages, the
+    value blocks then shifting the window's 128 newest rows to the front of
+    the 256-row value buffer), each timed as bursts of `reps` back-to-back
+    launches over 8 rotating input / page sets."""
     from kitty.kernels.ops import QuantizePlan, pool_store
     sets = 8
     n = B * sets
@@ -482,12 +497,18 @@ def spill_latency(torch, dev, B: int = 16, Hkv: int = 8, dk: int = 16, reps: int
         bi[h, torch.randperm(D, generator=torch.Generator().manual_seed(h))[:dk]] = torch.arange(dk, dtype=torch.uint8)
     bi = bi.to(dev)
     res = {}
-    for kind in ("key+value", "key only", "value only"):
+    R = 128
+    for kind in ("key+value", "key only", "value only", "window spill"):
         plans = []
         for i in range(sets):
             k = torch.randn(B, Hkv, G, D, device=dev, generator=g).half()
-            v = torch.randn(B, Hkv, G, D, device=dev, generator=g).half()
+            v = torch.randn(B, Hkv, G + (R if kind == "window spill" else 0), D, device=dev, generator=g).half()
             pids = torch.arange(i * B, (i + 1) * B, dtype=torch.int32, device=dev)
+            if kind == "window spill":
+                vids = torch.arange(n - (i + 1) * B, n - i * B, dtype=torch.int32, device=dev)
+                plans.append(QuantizePlan(store, k, v[:, :, :G], bi, pids, dk + 1, value_page_ids=vids,
+                                          value_shift=R))
+                continue
             plans.append(QuantizePlan(store, k if kind != "value only" else None,
                                       v if kind != "key only" else None,
                                       bi if kind != "value only" else None, pids, dk + 1))

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define KITTY_ABI_VERSION 5
+#define KITTY_ABI_VERSION 6
 
 /* Element type of 16-bit data (the *_dtype fields below). */
 #define KITTY_DTYPE_F16 0
@@ -119,6 +119,15 @@ typedef struct {
     int32_t src_dtype; /* key / value blocks: KITTY_DTYPE_F16 or KITTY_DTYPE_BF16 (ABI version 3) */
     int32_t outer_per_seq;          /* 0, or pages per sequence (ABI version 5) */
     int64_t key_s_seq, value_s_seq; /* sequence strides when outer_per_seq > 0 */
+    /* ABI version 6, for a spill that quantises keys and values of the same
+     * sequences into different pages and then shifts the value window
+     * (pipeline.py:233-250) in the same launch: */
+    const int32_t *value_page_ids; /* [n_outer], device: value block o goes to page value_page_ids[o];
+                                      NULL: to page_ids[o] like its key block */
+    int32_t value_shift;           /* R in [0, page_tokens]: after reading its value rows, block (o, i)
+                                      moves rows G .. G + R - 1 of its value source to rows 0 .. R - 1
+                                      (the source is written: the value window's newest R values move
+                                      to the front of the buffer); 0: the source is only read */
 } kitty_quant_batch;
 
 int kitty_quantize_kv_blocks(const kitty_page_store *store, const kitty_quant_batch *batch,
@@ -320,6 +329,20 @@ typedef struct {
 } kitty_append_args;
 
 int kitty_append_tokens(const kitty_append_args *args, kitty_stream_t stream);
+
+/* ------------------------------------------------ spill bookkeeping
+ * The device side of the page-table and counter updates that
+ * KittyInferencePipeline._trigger_quantization makes on its host object
+ * (kitty/pipeline.py:183-256: the new page's entry, the reset buffer
+ * lengths), for a caller that keeps those tables on the device; the value
+ * window's shift is kitty_quant_batch.value_shift.  The list travels in the
+ * kernel arguments, so a spill needs no host-to-device copy, and the stores
+ * are ordered on the stream with the caller's quantize launches (ABI
+ * version 6): *addrs[i] = values[i] for i < n (host lists of device
+ * addresses, 4-byte aligned, distinct; n >= 0), in launches of at most
+ * KITTY_STORE_I32_MAX stores. */
+#define KITTY_STORE_I32_MAX 320
+int kitty_store_i32(int32_t *const *addrs, const int32_t *values, int32_t n, kitty_stream_t stream);
 
 /* ------------------------------------------- sensitivity accumulation
  * Replaces _ChannelAccumulator.update (kitty/sensitivity.py:46-61):

@@ -7,6 +7,8 @@
 // the caller (kitty_quantize_kv_blocks).
 #include "common.h"
 
+#include <algorithm>
+
 namespace kitty {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
@@ -86,6 +88,21 @@ __global__ __launch_bounds__(64) void append_tokens_kernel(kitty_append_args a)
 
 static bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Spill bookkeeping: a list that travels in the kernel arguments (at most
+// 4 KB), so the host's page-table and counter updates need no staging copy.
+struct StoreI32Args {
+    int32_t n;
+    int32_t value[KITTY_STORE_I32_MAX];
+    int32_t *addr[KITTY_STORE_I32_MAX];
+};
+static_assert(sizeof(StoreI32Args) <= 4096, "kernel arguments above 4 KB");
+
+__global__ __launch_bounds__(256) void store_i32_kernel(StoreI32Args a)
+{
+    for (int i = threadIdx.x; i < a.n; i += 256)
+        *a.addr[i] = a.value[i];
+}
+
 } // namespace kitty
 
 using namespace kitty;
@@ -123,4 +140,26 @@ extern "C" int kitty_append_tokens(const kitty_append_args *args, kitty_stream_t
         return fail(KITTY_E_INVALID, "append buffers must be 16-byte aligned");
     hipLaunchKernelGGL(append_tokens_kernel, dim3(a.batch), dim3(64), 0, (hipStream_t)stream, a);
     return check_launch("append_tokens_kernel");
+}
+
+extern "C" int kitty_store_i32(int32_t *const *addrs, const int32_t *values, int32_t n, kitty_stream_t stream)
+{
+    if (n < 0 || (n > 0 && (!addrs || !values)))
+        return fail(KITTY_E_INVALID, "kitty_store_i32: n < 0 or NULL list");
+    for (int32_t i = 0; i < n; ++i)
+        if (!addrs[i] || ((uintptr_t)addrs[i] & 3u))
+            return fail(KITTY_E_INVALID, "kitty_store_i32: NULL or misaligned address");
+    for (int32_t i0 = 0; i0 < n; i0 += KITTY_STORE_I32_MAX) {
+        StoreI32Args a;
+        a.n = std::min<int32_t>(KITTY_STORE_I32_MAX, n - i0);
+        for (int32_t i = 0; i < a.n; ++i) {
+            a.addr[i] = addrs[i0 + i];
+            a.value[i] = values[i0 + i];
+        }
+        hipLaunchKernelGGL(store_i32_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, a);
+        const int rc = check_launch("store_i32_kernel");
+        if (rc != KITTY_OK)
+            return rc;
+    }
+    return KITTY_OK;
 }

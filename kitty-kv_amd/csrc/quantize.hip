@@ -120,7 +120,7 @@ __device__ void quantize_value_block(const QuantLaunch &L, int o, int i, unsigne
     float *red_mx = red_mn + kQuantThreads;
 
     const uint16_t *src = qb.value + outer_offset(qb, o, qb.value_s_seq, qb.value_s_outer) + i * qb.value_s_inner;
-    const int32_t page = qb.page_ids[o];
+    const int32_t page = (qb.value_page_ids ? qb.value_page_ids : qb.page_ids)[o];
 
     const int nsl = kQuantThreads / G;
     const int t = tid % G, sl = tid / G;
@@ -141,30 +141,39 @@ __device__ void quantize_value_block(const QuantLaunch &L, int o, int i, unsigne
     red_mn[tid] = mn;
     red_mx[tid] = mx;
     __syncthreads();
-    if (!active)
-        return;
-    for (int s2 = 0; s2 < nsl; ++s2) {
-        float a = red_mn[s2 * G + t], b = red_mx[s2 * G + t];
-        mn = a < mn ? a : mn;
-        mx = b > mx ? b : mx;
-    }
-    float rng = mx - mn;                                           // quantize_value.py:65
-    if (rng < 1e-8f)
-        rng = 1e-8f;
-    const float s = rng / 3.0f;                                    // :67
-    const float z = zp_clamp(__builtin_rintf(-mn / s), 3.0f);      // :69-73
-    uint8_t *row = st.value + page * st.value_s_page + i * st.value_s_head + t * st.value_s_row;
-    for (int j = j0; j < j1; ++j) {                                // :78-88
-        uint32_t byte = 0;
+    if (active) {
+        for (int s2 = 0; s2 < nsl; ++s2) {
+            float a = red_mn[s2 * G + t], b = red_mx[s2 * G + t];
+            mn = a < mn ? a : mn;
+            mx = b > mx ? b : mx;
+        }
+        float rng = mx - mn;                                       // quantize_value.py:65
+        if (rng < 1e-8f)
+            rng = 1e-8f;
+        const float s = rng / 3.0f;                                // :67
+        const float z = zp_clamp(__builtin_rintf(-mn / s), 3.0f);  // :69-73
+        uint8_t *row = st.value + page * st.value_s_page + i * st.value_s_head + t * st.value_s_row;
+        for (int j = j0; j < j1; ++j) {                            // :78-88
+            uint32_t byte = 0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            byte |= quant_code(load(4 * j + k), s, z, 3.0f) << (2 * k);
-        row[j] = (uint8_t)byte;
+            for (int k = 0; k < 4; ++k)
+                byte |= quant_code(load(4 * j + k), s, z, 3.0f) << (2 * k);
+            row[j] = (uint8_t)byte;
+        }
+        if (sl == 0) {                                             // :90
+            const int64_t m = page * st.value_meta_s_page + i * st.value_meta_s_head + t * st.value_meta_s_tok;
+            st.value_scale[m] = meta_store(s, mbf);
+            st.value_zero[m] = meta_store(z, mbf);
+        }
     }
-    if (sl == 0) {                                                 // :90
-        const int64_t m = page * st.value_meta_s_page + i * st.value_meta_s_head + t * st.value_meta_s_tok;
-        st.value_scale[m] = meta_store(s, mbf);
-        st.value_zero[m] = meta_store(z, mbf);
+    if (qb.value_shift > 0) {   // the window's newest R rows to the front, once every row above is read
+        __syncthreads();
+        uint16_t *buf = const_cast<uint16_t *>(src);
+        for (int e = tid; e < qb.value_shift * D; e += kQuantThreads) {
+            const int r = e / D, d = e - r * D;
+            buf[(int64_t)r * qb.value_s_tok + (int64_t)d * qb.value_s_chan] =
+                src[(int64_t)(G + r) * qb.value_s_tok + (int64_t)d * qb.value_s_chan];
+        }
     }
 }
 
@@ -173,9 +182,9 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_kv_kernel(QuantLaunch 
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int n = blockIdx.x;
     const int o = n / L.qb.n_inner, i = n - o * L.qb.n_inner;
-    const int32_t page = L.qb.page_ids[o];
+    const int32_t page = (blockIdx.y == 1 && L.qb.value_page_ids ? L.qb.value_page_ids : L.qb.page_ids)[o];
     if (page < 0 || page >= L.st.num_pages || i >= L.st.num_kv_heads)
-        return; // never write outside the pools
+        return; // never write outside the pools (nor shift a block whose page is refused)
     if (blockIdx.y == 0) {
         if (L.qb.key)
             quantize_key_block(L, o, i, smem);
@@ -278,6 +287,10 @@ extern "C" int kitty_quantize_kv_blocks(const kitty_page_store *store, const kit
         return fail(KITTY_E_INVALID, "value_rows must be in [0, page_tokens]");
     if (qb.src_dtype != KITTY_DTYPE_F16 && qb.src_dtype != KITTY_DTYPE_BF16)
         return fail(KITTY_E_INVALID, "src_dtype must be KITTY_DTYPE_F16 or KITTY_DTYPE_BF16");
+    if (qb.value_shift < 0 || qb.value_shift > store->page_tokens)
+        return fail(KITTY_E_INVALID, "value_shift must be in [0, page_tokens]");
+    if (qb.value_shift > 0 && !qb.value)
+        return fail(KITTY_E_INVALID, "value_shift needs value blocks");
     const int D = store->head_dim, G = store->page_tokens;
     const size_t key_lds = (size_t)G * D * 2 + ((D + 15) & ~15) + (((size_t)D * (G / 4) + 15) & ~15) +
                            2 * kQuantThreads * sizeof(float);

@@ -253,12 +253,13 @@ __device__ __forceinline__ void readn(const unsigned char *lds, int off, T (&v)[
     }
 }
 
-// Destination page of block (o, i), looked up after the block's loads are
-// issued so that they do not wait for it.  A page id outside the pool, or a
-// head past the pool's heads, writes nothing (never outside the pools).
-__device__ __forceinline__ int64_t dest_page(const QuantLaunch &L, int o, int i, bool &ok)
+// Destination page of block (o, i) of a role (values may have a page list of
+// their own), looked up after the block's loads are issued so that they do
+// not wait for it.  A page id outside the pool, or a head past the pool's
+// heads, writes nothing (never outside the pools).
+__device__ __forceinline__ int64_t dest_page(const QuantLaunch &L, int o, int i, bool value_role, bool &ok)
 {
-    const int64_t page = L.qb.page_ids[o];
+    const int64_t page = (value_role && L.qb.value_page_ids ? L.qb.value_page_ids : L.qb.page_ids)[o];
     ok = page >= 0 && page < L.st.num_pages && i < L.st.num_kv_heads;
     return page;
 }
@@ -301,7 +302,7 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
     // boost rank of channel tid (threads 128.. load a copy and ignore it)
     const int b = qb.boost_idx[o * qb.boost_s_outer + i * qb.boost_s_inner + (tid & 127)];
     bool ok;
-    const int64_t page = dest_page(L, o, i, ok);
+    const int64_t page = dest_page(L, o, i, false, ok);
 
     unsigned *high = (unsigned *)(lds + kHighOff);
     for (int e = tid; e < Dk * 8; e += kThreads)
@@ -421,11 +422,11 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cg = lane & 15, tt = wave * 4 + (lane >> 4);
 
+    const uint16_t *vsrc = qb.value + outer_offset(qb, o, qb.value_s_seq, qb.value_s_outer) + i * qb.value_s_inner;
     u32x4 r[kTok];
-    load_rows(qb.value + outer_offset(qb, o, qb.value_s_seq, qb.value_s_outer) + i * qb.value_s_inner + 8 * cg, qb.value_s_tok, kTok * tt,
-              qb.value_rows, cg, r);
+    load_rows(vsrc + 8 * cg, qb.value_s_tok, kTok * tt, qb.value_rows, cg, r);
     bool ok;
-    const int64_t page = dest_page(L, o, i, ok);
+    const int64_t page = dest_page(L, o, i, true, ok);
 
     // (min, -max) of each token over the thread's 8 channels, packed in fp16
     // (:63-64): min over the four channel pairs, the same over the negated
@@ -469,6 +470,19 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
     }
     __syncthreads();
 
+    // value_shift: every row of the block has been read (above the barrier);
+    // rows G .. G + R - 1 are loaded now and stored to rows 0 .. R - 1 after
+    // the codes, one 16-byte vector of a 256-byte row per (thread, u)
+    const int R = ok ? qb.value_shift : 0;
+    u32x4 shifted[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int e = tid + u * kThreads;
+        if (e < R * 16)
+            shifted[u] = __builtin_nontemporal_load((const u32x4 *)(vsrc + (int64_t)(128 + (e >> 4)) * qb.value_s_tok +
+                                                                     8 * (e & 15)));
+    }
+
     float s[kTok], rs[kTok], z[kTok];
     readn<kTok>(lds, kParOff + 4 * kTok * tt, s);
     readn<kTok>(lds, kParOff + 512 + 4 * kTok * tt, rs);
@@ -502,6 +516,12 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
     __syncthreads();
     if (ok)
         store_tile(st.value + page * st.value_s_page + i * st.value_s_head, lds, tid);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int e = tid + u * kThreads;
+        if (e < R * 16)
+            *(u32x4 *)(const_cast<uint16_t *>(vsrc) + (int64_t)(e >> 4) * qb.value_s_tok + 8 * (e & 15)) = shifted[u];
+    }
 }
 
 __global__ __launch_bounds__(kThreads) void quantize_page128_kernel(QuantLaunch L)

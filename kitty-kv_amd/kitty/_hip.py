@@ -19,7 +19,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 # KITTY_HIP_LIBRARY selects another build of the same ABI (e.g. a tuning variant).
 LIB_PATH = os.environ.get("KITTY_HIP_LIBRARY") or os.path.join(_HERE, "libkitty_hip.so")
 
-KITTY_ABI_VERSION = 5
+KITTY_ABI_VERSION = 6
 KITTY_OK = 0
 KITTY_E_INVALID = -1
 KITTY_E_HIP = -2
@@ -72,6 +72,7 @@ class QuantBatch(ctypes.Structure):
         ("boost_idx", _vp), ("boost_s_outer", _i64), ("boost_s_inner", _i64),
         ("page_ids", _vp), ("n_outer", _i32), ("n_inner", _i32), ("value_rows", _i32), ("sentinel", _i32),
         ("src_dtype", _i32), ("outer_per_seq", _i32), ("key_s_seq", _i64), ("value_s_seq", _i64),
+        ("value_page_ids", _vp), ("value_shift", _i32),
     ]
 
 
@@ -123,7 +124,7 @@ EXPORTED_SYMBOLS = (
     "kitty_decode_workspace_size", "kitty_decode_path", "kitty_paged_decode", "kitty_paged_decode_splits",
     "kitty_paged_decode_merge", "kitty_paged_decode_noalloc", "kitty_append_tokens", "kitty_channel_abs_sum",
     "kitty_channel_abs_sum_workspace_size", "kitty_channel_abs_sum_deferred_size", "kitty_channel_abs_sum_deferred",
-    "kitty_channel_abs_sum_flush",
+    "kitty_channel_abs_sum_flush", "kitty_store_i32",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -161,6 +162,7 @@ def load() -> ctypes.CDLL:
     L.kitty_channel_abs_sum_deferred_size.argtypes = [_i32, _i32, ctypes.POINTER(ctypes.c_size_t)]
     L.kitty_channel_abs_sum_deferred.argtypes = L.kitty_channel_abs_sum.argtypes
     L.kitty_channel_abs_sum_flush.argtypes = [_vp, _i32, _i32, _vp, _vp]
+    L.kitty_store_i32.argtypes = [_vp, _vp, _i32, _vp]
     if L.kitty_abi_version() != KITTY_ABI_VERSION:
         raise ImportError(f"libkitty_hip ABI {L.kitty_abi_version()} != {KITTY_ABI_VERSION}")
     _lib = L

@@ -78,10 +78,11 @@ def pool_store(key_baseline: torch.Tensor, key_boost: torch.Tensor, key_meta: to
 
 def _quant_batch(store: _hip.PageStore, key: Optional[torch.Tensor], value: Optional[torch.Tensor],
                  boost_idx: Optional[torch.Tensor], page_ids: torch.Tensor, sentinel: int,
-                 value_rows: Optional[int]) -> Tuple[_hip.QuantBatch, torch.device]:
+                 value_rows: Optional[int], value_page_ids: Optional[torch.Tensor] = None,
+                 value_shift: int = 0) -> Tuple[_hip.QuantBatch, torch.device]:
     ref = key if key is not None else value
     _need(ref is not None, "nothing to quantise")
-    dev = _hip.require_device(key, value, boost_idx, page_ids)
+    dev = _hip.require_device(key, value, boost_idx, page_ids, value_page_ids)
     _need(ref.dim() in (4, 5), "key / value blocks must be (n_outer, H, G, D) or (n_seq, pages, H, G, D)")
     per_seq = ref.shape[1] if ref.dim() == 5 else 0
     n_outer = ref.shape[0] * per_seq if per_seq else ref.shape[0]
@@ -120,6 +121,19 @@ def _quant_batch(store: _hip.PageStore, key: Optional[torch.Tensor], value: Opti
     b.n_outer, b.n_inner = n_outer, n_inner
     b.value_rows = G if value_rows is None else int(value_rows)
     b.sentinel = int(sentinel)
+    if value_page_ids is not None:
+        _need(value is not None and value_page_ids.dtype == torch.int32 and value_page_ids.numel() == n_outer
+              and value_page_ids.is_contiguous(), "value_page_ids must be int32 (n_outer,) with value blocks")
+        b.value_page_ids = value_page_ids.data_ptr()
+    if value_shift:
+        _need(value is not None and 0 < value_shift <= G, "value_shift must be in [0, G] with value blocks")
+        # the shift reads rows G .. G + value_shift - 1 past each value block: they must be in its storage
+        _need(min(value.stride()) >= 0, "value_shift needs non-negative value strides")
+        last = value.storage_offset() + sum((n - 1) * st for n, st in zip(value.shape, value.stride())) \
+            + value_shift * value.stride(-2)
+        _need(last < value.untyped_storage().nbytes() // value.element_size(),
+              "value_shift: rows G .. G + value_shift - 1 of a value block lie outside its tensor's storage")
+        b.value_shift = int(value_shift)
     return b, dev
 
 
@@ -150,10 +164,16 @@ class QuantizePlan:
 
     def __init__(self, store: _hip.PageStore, key: Optional[torch.Tensor], value: Optional[torch.Tensor],
                  boost_idx: Optional[torch.Tensor], page_ids: torch.Tensor, sentinel: int,
-                 value_rows: Optional[int] = None) -> None:
-        self._b, self._dev = _quant_batch(store, key, value, boost_idx, page_ids, sentinel, value_rows)
+                 value_rows: Optional[int] = None, value_page_ids: Optional[torch.Tensor] = None,
+                 value_shift: int = 0) -> None:
+        """value_page_ids: the value blocks' own pages (default page_ids);
+        value_shift R > 0: after reading its value rows, each value block
+        moves rows G .. G + R - 1 of its source to rows 0 .. R - 1 (the value
+        window shift of a spill; the source's storage must hold those rows)."""
+        self._b, self._dev = _quant_batch(store, key, value, boost_idx, page_ids, sentinel, value_rows,
+                                          value_page_ids, value_shift)
         self._store = store
-        self._keep = (key, value, boost_idx, page_ids)
+        self._keep = (key, value, boost_idx, page_ids, value_page_ids)
         self._lib = _hip.load()
 
     def run(self) -> None:

@@ -31,19 +31,23 @@ On a ROCm device the hot path of a decode step is:
   sequence of the batch into its sink, key and value buffers and advances the
   device-side counters (``lens``: sink fill, key buffer length, key pages,
   value pages, value buffer length per (layer, slot));
-* for the sequences whose key buffer became full, one key-only
-  ``kitty_quantize_kv_blocks`` launch into freshly allocated pages; for those
-  whose value buffer reached R + G rows, one value-only launch into the value
-  half of their oldest value-less page, then a device-side shift of the
-  remaining R values (R = 0: one launch for both);
+* for the sequences whose key buffer became full, a ``kitty_quantize_kv_blocks``
+  launch of their keys into freshly allocated pages; for those whose value
+  buffer reached R + G rows, of their oldest G values into the value half of
+  their oldest value-less page, the same launch's value blocks then moving
+  the R newest values to the front of the buffer (one launch when the two
+  sets are the same run of slots, as with R = G or R = 0);
 * the decode reads lengths, block table rows and FP16 segments straight from
   these device tensors.
 
 Host state mirrors the counters (every push adds exactly one token per
 sequence, so the host knows when a buffer fills without reading the device);
-nothing here waits for the GPU: the few host-side integers a spill needs on
-the device (slots, page ids, page numbers) go through pinned memory with
-non-blocking copies on the current stream.  A prompt (T > 1 tokens) goes
+nothing here waits for the GPU.  The few integers a spill changes on the
+device (the new pages' ids, block-table entries, counters) travel in the
+kernel arguments of one ``kitty_store_i32`` launch when the spilled slots are
+ascending runs (every single sequence, and sequences in lockstep); other slot
+sets stage their metadata through pinned memory with a non-blocking copy on
+the current stream.  A prompt (T > 1 tokens) goes
 through ``push_chunk``: sinks and buffer rows are copied in bulk and every
 complete G-token page of the chunk is quantised straight from it.
 """
@@ -116,6 +120,9 @@ class KittyInferencePipeline:
         # per (layer, first slot, count, kind): the quantise launch of a spill
         # of that run of slots, validated once (page ids read from _spill_ids)
         self._spill_plans: Dict[Tuple[int, int, int, str], object] = {}
+        # _spill_one's store list (reused)
+        self._one_addrs = (ctypes.c_int64 * 8)()
+        self._one_vals = (ctypes.c_int32 * 8)()
         self._on_device = dev.type == "cuda"
         if self._on_device:
             self._lib = _hip.load()
@@ -237,7 +244,12 @@ class KittyInferencePipeline:
             in_sink = self._fill[s, l] < S
             kf = not in_sink and self._qlen[s, l] + 1 == G
             vf = not in_sink and self._vlen[s, l] + 1 == self.value_capacity
-            phys = self._alloc_spill(l, slots, [ids[0]]) if kf else []
+            phys = []
+            if kf:      # _alloc_spill for one page of one sequence
+                pno = int(self._npages[s, l])
+                if pno + 1 > self.max_pages_per_seq:
+                    raise RuntimeError(f"sequence {ids[0]} exceeds max_seq_len={cfg.max_seq_len}")
+                phys = self.layout.allocate_run(ids[0], l, pno, 1)
             append(l, keys, values, slots)
             if in_sink:
                 self._fill[s, l] += 1
@@ -245,7 +257,10 @@ class KittyInferencePipeline:
                 self._qlen[s, l] += 1
                 self._vlen[s, l] += 1
             if kf or vf:
-                self._spill(l, slots if kf else slots[:0], phys, slots if vf else slots[:0])
+                if self._on_device and cfg.local_value_window <= G:
+                    self._spill_one(l, s, kf, vf, phys)
+                else:
+                    self._spill(l, slots if kf else slots[:0], phys, slots if vf else slots[:0])
             return
         fill = self._fill[slots, l]
         in_sink = fill < S
@@ -374,7 +389,15 @@ class KittyInferencePipeline:
         if v:
             self._npv[vslots, layer] += 1
             self._vlen[vslots, layer] -= G
-        touched = np.union1d(kslots, vslots[:v]).astype(np.int64)
+        if v == 0:
+            touched = np.asarray(kslots, np.int64)
+        elif k == 0 or (k == v and np.array_equal(kslots, vslots)):
+            touched = np.asarray(vslots[:v], np.int64)
+        else:
+            touched = np.union1d(kslots, vslots[:v]).astype(np.int64)
+        if self._on_device and R <= G and (k == 0 or _is_run(kslots)) and (v == 0 or _is_run(vslots[:v])):
+            self._spill_runs(layer, kslots, np.asarray(phys, np.int64), pno, vslots[:v], vphys, touched, both)
+            return
         lens_new = self._counts[:, touched, layer]
         nt = len(touched)
         # staged int32: key page ids at [0, k), value page ids at [n, n + v)
@@ -435,6 +458,87 @@ class KittyInferencePipeline:
         else:
             self.lens[:, layer, tsl] = lens_dev
 
+    def _spill_runs(self, layer: int, kslots: np.ndarray, phys: np.ndarray, pno: np.ndarray, vslots: np.ndarray,
+                    vphys: np.ndarray, touched: np.ndarray, both: bool) -> None:
+        """The device side of a spill whose key and value slots are ascending
+        runs (every single sequence, and sequences in lockstep), with R <= G:
+        one kitty_store_i32 launch writes the page ids the cached quantise
+        launches read, the new block-table entries and the touched slots'
+        counters, all carried in its kernel arguments (no staging copy);
+        then one quantise launch for keys and values of the same run (key
+        pages and value pages of their own), or one each, whose value blocks
+        also move the window's R newest values to the front of the value
+        buffer after reading the oldest G (kitty_quant_batch.value_shift)."""
+        cfg = self.config
+        G, R = cfg.q_buffer_size, cfg.local_value_window
+        n, L, maxp = self.num_slots, cfg.num_layers, self.max_pages_per_seq
+        k, v, nt = len(kslots), len(vslots), len(touched)
+        if self._meta_dev is None:
+            self._meta_dev = torch.zeros(16 + 12 * n, dtype=torch.int32, device=self.device)
+        meta = self._meta_dev
+        mp, bp, lp = meta.data_ptr(), self._block_table.data_ptr(), self.lens.data_ptr()
+        addrs = np.empty(2 * k + v + 5 * nt, np.int64)
+        vals = np.empty(len(addrs), np.int32)
+        addrs[:k] = mp + 4 * np.arange(k)
+        vals[:k] = phys
+        addrs[k:k + v] = mp + 4 * (n + np.arange(v))
+        vals[k:k + v] = vphys
+        addrs[k + v:2 * k + v] = bp + 4 * ((layer * n + np.asarray(kslots, np.int64)) * maxp + pno)
+        vals[k + v:2 * k + v] = phys
+        addrs[2 * k + v:] = (lp + 4 * ((np.arange(5)[:, None] * L + layer) * n + touched[None, :])).ravel()
+        vals[2 * k + v:] = self._counts[:, touched, layer].ravel()
+        _hip.check(self._lib.kitty_store_i32(addrs.ctypes.data, vals.ctypes.data, len(addrs),
+                                             _hip.stream_ptr(self.device)))
+        if k and v and k == v and kslots[0] == vslots[0]:     # the same run: one launch for keys and values
+            self._run_plan(layer, int(kslots[0]), k, "kvs", meta).run()
+            return
+        if k:
+            self._run_plan(layer, int(kslots[0]), k, "kv" if both else "k", meta).run()
+        if v:
+            self._run_plan(layer, int(vslots[0]), v, "vs" if R else "v", meta).run()
+
+    def _spill_one(self, layer: int, s: int, kf: bool, vf: bool, phys: List[int]) -> None:
+        """_spill_runs for one sequence (slot s), on Python scalars: the
+        same host counter updates and the same two launches, with the store
+        list built in reused ctypes arrays."""
+        cfg = self.config
+        G, R = cfg.q_buffer_size, cfg.local_value_window
+        both = R == 0
+        n, L = self.num_slots, cfg.num_layers
+        if self._meta_dev is None:
+            self._meta_dev = torch.zeros(16 + 12 * n, dtype=torch.int32, device=self.device)
+        meta = self._meta_dev
+        addrs, vals = self._one_addrs, self._one_vals
+        mp = meta.data_ptr()
+        m = 0
+        if kf:
+            page = int(phys[0])
+            pno = int(self._npages[s, layer])
+            self._pages[s, layer, pno] = page
+            self._npages[s, layer] = pno + 1
+            self._qlen[s, layer] = 0
+            addrs[0], vals[0] = mp, page
+            addrs[1] = self._block_table.data_ptr() + 4 * ((layer * n + s) * self.max_pages_per_seq + pno)
+            vals[1] = page
+            m = 2
+            if both:
+                self._npv[s, layer] += 1
+                self._vlen[s, layer] = 0
+        vf = vf and not both
+        if vf:
+            npv = int(self._npv[s, layer])
+            addrs[m], vals[m] = mp + 4 * n, int(self._pages[s, layer, npv])
+            m += 1
+            self._npv[s, layer] = npv + 1
+            self._vlen[s, layer] -= G
+        lp = self.lens.data_ptr() + 4 * (layer * n + s)
+        for c in range(5):
+            addrs[m + c] = lp + 4 * c * L * n
+            vals[m + c] = int(self._counts[c, s, layer])
+        _hip.check(self._lib.kitty_store_i32(addrs, vals, m + 5, _hip.stream_ptr(self.device)))
+        kind = ("kvs" if vf else "k") if kf and not both else ("kv" if kf else ("vs" if R else "v"))
+        self._run_plan(layer, s, 1, kind, meta).run()
+
     def _stage_meta(self, host: np.ndarray) -> torch.Tensor:
         """A spill's int32 metadata on the device, in a buffer of fixed
         address (the cached launches of _run_plan read their page ids from
@@ -448,19 +552,22 @@ class KittyInferencePipeline:
         return self._meta_dev
 
     def _run_plan(self, layer: int, a: int, count: int, kind: str, meta: torch.Tensor):
-        """The quantise launch of a spill of slots [a, a + count) at a layer:
-        "k" (keys into the pages at meta[0:count]), "kv" (keys and values, R =
-        0) or "v" (values into the pages at meta[n:n + count]), validated
-        once and kept."""
+        """The quantise launch of a spill of slots [a, a + count) at a layer,
+        validated once and kept: "k" (keys into the pages at meta[0:count]),
+        "kv" (keys and values into those pages, R = 0), "v" (values into the
+        pages at meta[n:n + count]), "vs" (the same, then the R-row window
+        shift of each value block) or "kvs" (keys into meta[0:count], values
+        into meta[n:n + count], then the shift)."""
         key = (layer, a, count, kind)
         plan = self._spill_plans.get(key)
         if plan is None:
-            G, n = self.config.q_buffer_size, self.num_slots
-            kb = self._qbuf_k[a:a + count, layer] if kind in ("k", "kv") else None
-            vb = self._vbuf[a:a + count, layer, :, :G] if kind in ("kv", "v") else None
-            ids = meta[n:n + count] if kind == "v" else meta[:count]
+            G, n, R = self.config.q_buffer_size, self.num_slots, self.config.local_value_window
+            kb = self._qbuf_k[a:a + count, layer] if kind in ("k", "kv", "kvs") else None
+            vb = self._vbuf[a:a + count, layer, :, :G] if kind != "k" else None
+            ids = meta[n:n + count] if kind in ("v", "vs") else meta[:count]
             plan = QuantizePlan(self._store, kb, vb, self.boost_idx_uint8[layer] if kb is not None else None, ids,
-                                self.config.sentinel)
+                                self.config.sentinel, value_page_ids=meta[n:n + count] if kind == "kvs" else None,
+                                value_shift=R if kind in ("vs", "kvs") else 0)
             if len(self._spill_plans) >= 256:
                 self._spill_plans.clear()
             self._spill_plans[key] = plan

@@ -44,11 +44,25 @@ def test_invalid_arguments_are_rejected_without_launch():
     b.n_outer, b.n_inner, b.page_ids, b.outer_per_seq = 1, 1, 16, -1   # the id pointer is never read here
     assert L.kitty_quantize_kv_blocks(ctypes.byref(st), ctypes.byref(b), None) == _hip.KITTY_E_INVALID
     assert b"outer_per_seq" in L.kitty_last_error()
+    b.outer_per_seq, b.value_shift = 0, 129
+    assert L.kitty_quantize_kv_blocks(ctypes.byref(st), ctypes.byref(b), None) == _hip.KITTY_E_INVALID
+    assert b"value_shift" in L.kitty_last_error()
+    b.value_shift = 64                                                  # no value blocks to shift
+    assert L.kitty_quantize_kv_blocks(ctypes.byref(st), ctypes.byref(b), None) == _hip.KITTY_E_INVALID
+    assert b"value_shift needs" in L.kitty_last_error()
     a = _hip.DecodeArgs()
     a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.page_tokens = 1, 6, 4, 128, 128
     assert L.kitty_paged_decode(ctypes.byref(a), None) == _hip.KITTY_E_INVALID
     a.num_q_heads, a.head_dim = 8, 512
     assert L.kitty_paged_decode(ctypes.byref(a), None) == _hip.KITTY_E_UNSUPPORTED
+    # spill bookkeeping: bad lists fail before any launch; empty lists are no-ops
+    import numpy as np
+    addrs = np.array([0x1000, 0x1002], np.int64)       # never dereferenced: the second is misaligned
+    vals = np.array([1, 2], np.int32)
+    assert L.kitty_store_i32(addrs.ctypes.data, vals.ctypes.data, 2, None) == _hip.KITTY_E_INVALID
+    assert b"misaligned" in L.kitty_last_error()
+    assert L.kitty_store_i32(None, None, -1, None) == _hip.KITTY_E_INVALID
+    assert L.kitty_store_i32(None, None, 0, None) == _hip.KITTY_OK
     with pytest.raises(NotImplementedError):
         _hip.check(_hip.KITTY_E_UNSUPPORTED)
     with pytest.raises(RuntimeError):
