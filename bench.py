@@ -20,9 +20,14 @@ events on the launch stream, right after `value` at the same settled clock
 (per-launch event pairs in the alternating step pattern are reported as
 upper bounds).
 
-`legs` repeats this for configs 4 and 5, each with its own roofline block;
-`quantize_pack` times config 2's batch quantize, `spill` the pipeline's spill
-launch, `module_forward` KittyPagedAttention.forward decode steps;
+`value_window_r128` times the same step in the layout the pipeline decodes
+with its 128-token FP16 value window (one value page fewer per sequence, a
+224-token value tail); `legs` repeats the headline for configs 4 and 5, each
+with its own roofline block and a sampled CPU baseline; `quantize_pack` times
+config 2's batch quantize, `spill` the pipeline's spill launch,
+`module_forward` KittyPagedAttention.forward decode steps on the GPU and
+`module_forward_cfg1_cpu` the same module on CPU tensors (the product's CPU
+path);
 `reference_items` runs the reference's own benchmark items (one-page key
 quantise / dequantise, push_token throughput, memory compression) with its
 defaults and timing method, and `widened_rows` times prefill (push_chunk) and
@@ -471,6 +476,49 @@ def module_leg(torch, dev, cfg_name: str = "cfg3", cycles: int = 2, event_cycles
                     "spill_step_us: median of the spill steps; cycle_max_step_us: median over cycles of each "
                     "cycle's largest step, spill or not (host noise included); host clock over the timed steps "
                     "includes the Python module overhead"}
+
+
+def module_leg_cpu(torch, cfg_name: str = "cfg1", steps: int = 256) -> dict:
+    """KittyPagedAttention.forward decode steps with every tensor on the CPU
+    (the product's own CPU path, kitty/kernels/cpu.py: quantise, spills and
+    decode in torch), at config 1's shape: one sequence prefilled to
+    ctx - 2G tokens with push_chunk, then `steps` decode steps (two spill
+    cycles), host clock, on every thread torch may use here."""
+    from kitty import KittyConfig, KittyAttentionFactory
+    c = CONFIGS[cfg_name]
+    B, Hq, Hkv, ctx = c["B"], c["Hq"], c["Hkv"], c["ctx"]
+    threads = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        kcfg = KittyConfig(num_layers=1, num_kv_heads=Hkv, head_dim=D, q_buffer_size=G, sink_size=S,
+                           local_value_window=128, boost_rate=c["boost"], max_seq_len=ctx + 4 * G,
+                           max_batch_size=B, device="cpu")
+        gen = torch.Generator().manual_seed(c["seed"])
+        bi = torch.full((1, Hkv, D), kcfg.sentinel, dtype=torch.uint8)
+        for h in range(Hkv):
+            bi[0, h, torch.randperm(D, generator=gen)[:kcfg.d_boost]] = torch.arange(kcfg.d_boost, dtype=torch.uint8)
+        layout, pipe, layers = KittyAttentionFactory.from_config(kcfg, bi, Hq)
+        attn = layers[0]
+        k = torch.randn(B, Hkv, ctx - 2 * G, D, generator=gen).half()
+        v = torch.randn(B, Hkv, ctx - 2 * G, D, generator=gen).half()
+        pipe.push_chunk(0, k, v, list(range(B)))
+        qs = torch.randn(steps, B, Hq, 1, D, generator=gen).half()
+        ks = torch.randn(steps, B, Hkv, 1, D, generator=gen).half()
+        vs = torch.randn(steps, B, Hkv, 1, D, generator=gen).half()
+        per = []
+        for i in range(steps):
+            t0 = time.perf_counter()
+            attn(qs[i], ks[i], vs[i], seq_id=list(range(B)))
+            per.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
+    return {"workload": f"KittyPagedAttention.forward decode on CPU tensors, {cfg_name} shape: B{B} Hq{Hq} Hkv{Hkv} "
+                        f"d{D}, contexts {ctx - 2 * G + 1}..{ctx - 2 * G + steps}, S{S} G{G} R128",
+            "us_per_step": round(sum(per) / steps * 1e6, 1), "us_per_step_median": round(statistics.median(per) * 1e6, 1),
+            "steps": steps, "cores": threads, **host_cpu(),
+            "note": "kitty/kernels/cpu.py through the module and pipeline (no oracle): bit-exact quantisation, "
+                    "fp32 decode; host clock per step"}
 
 
 def spill_latency(torch, dev, B: int = 16, Hkv: int = 8, dk: int = 16, reps: int = 64) -> dict:
@@ -992,6 +1040,8 @@ def main() -> int:
         log("timing KittyPagedAttention.forward decode steps")
         result["module_forward"] = module_leg(torch, dev, "cfg3")
         result["module_forward_cfg1"] = module_leg(torch, dev, "cfg1")
+        log("timing the module on CPU tensors (config 1)")
+        result["module_forward_cfg1_cpu"] = module_leg_cpu(torch)
     if not args.no_extra:
         log("timing the reference benchmark's items, prefill and the profiler accumulation")
         result["reference_items"] = reference_items(torch, dev)
