@@ -970,6 +970,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-quantize", action="store_true")
     ap.add_argument("--no-module", action="store_true", help="skip the KittyPagedAttention.forward leg")
+    ap.add_argument("--no-window", action="store_true", help="skip the config-3 value-window decode leg")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the reference benchmark's items and the prefill / profiler rows")
     ap.add_argument("--copy-probe", action="store_true",
@@ -1013,7 +1014,7 @@ def main() -> int:
         "step_us_events": main_rec["step_us_events"],
         "roofline": main_rec["roofline"],
     }
-    if args.config == "cfg3":
+    if args.config == "cfg3" and not args.no_window:
         result["value_window_r128"] = window_leg(torch, w, K, args.warmup, max(0.5, args.warmup_seconds / 2))
     if not args.no_cpu_baseline:
         log(f"timing CPU baselines ({cpu_threads()} torch threads, then the C port on 1 thread)")
