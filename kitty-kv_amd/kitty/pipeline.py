@@ -118,7 +118,7 @@ class KittyInferencePipeline:
         self._stager = None         # pinned staging rows of _h2d, allocated on first use
         self._meta_dev = None       # a spill's staged metadata (fixed address, see _stage_meta)
         # per (layer, first slot, count, kind): the quantise launch of a spill
-        # of that run of slots, validated once (page ids read from _spill_ids)
+        # of that run of slots, validated once (page ids read from _meta_dev)
         self._spill_plans: Dict[Tuple[int, int, int, str], object] = {}
         # _spill_one's store list (reused)
         self._one_addrs = (ctypes.c_int64 * 8)()
@@ -362,17 +362,18 @@ class KittyInferencePipeline:
     def _spill(self, layer: int, kslots: np.ndarray, phys: List[int], vslots: np.ndarray) -> None:
         """Key spill of kslots (their full key buffers into the new pages
         phys, one each) and value spill of vslots (the oldest G values into
-        the value half of their first value-less page) (pipeline.py:183-256).
-        One launch each; one launch for both when R = 0 (the same slots and
-        pages).  The host counters are advanced first; their new values for
-        every touched slot travel to the device with the slots and page ids
-        in one pinned copy and land in one write.
+        the value half of their first value-less page, then the R newest
+        values to the front of the buffer) (pipeline.py:183-256).  The host
+        counters are advanced first.
 
-        Host cost: a run of ascending slots (sequences that advance in
-        lockstep, and every single sequence) quantises through launches
-        validated once per (layer, run) that read their page ids from a fixed
-        device buffer, and updates the block table and counters with slice
-        copies; other slot sets gather their rows and use indexed writes."""
+        On the device, when both slot sets are ascending runs (sequences that
+        advance in lockstep, and every single sequence) and R <= G, the work
+        is _spill_runs: the new ids, block-table entries and counters in one
+        kitty_store_i32 launch and the quantise launches cached per (layer,
+        run), the value window's shift inside the value launch.  Otherwise
+        (other slot sets, R > G, CPU pools) the new counters, slots and page
+        ids go to the device in one pinned copy; the blocks are gathered, and
+        the block table, counters and value shift are indexed torch writes."""
         G, R = self.config.q_buffer_size, self.config.local_value_window
         both = R == 0
         k, v = len(kslots), (0 if both else len(vslots))
