@@ -27,7 +27,7 @@ with its own roofline block and a sampled CPU baseline; `quantize_pack` times
 config 2's batch quantize, `spill` the pipeline's spill launch,
 `module_forward` KittyPagedAttention.forward decode steps on the GPU and
 `module_forward_cfg1_cpu` the same module on CPU tensors (the product's CPU
-path);
+path), with `cpu_baseline_cfg1` the reference's CPU decode of config 1 beside it;
 `reference_items` runs the reference's own benchmark items (one-page key
 quantise / dequantise, push_token throughput, memory compression) with its
 defaults and timing method, and `widened_rows` times prefill (push_chunk) and
@@ -221,6 +221,39 @@ def cpu_baseline_torch(w, budget_s: float) -> dict:
                       f"{w['Hkv']} KV heads, {S} sinks + FP16 tail each) through oracle/torch_reference.py "
                       f"(paged_attention_reference restated op for op in torch, CPU, {threads} threads); "
                       f"scaled by pages to one layer-step"}
+
+
+def cpu_baseline_cfg1(torch, dev, budget_s: float = 3.0) -> dict:
+    """The reference's CPU decode at config 1 (one sequence, 8 Q / 8 KV heads,
+    1K context): oracle/torch_reference.py's paged_attention (the reference's
+    paged_attention_reference restated op for op) on config 1's pools, run
+    repeatedly for about budget_s on every thread torch may use here; the
+    median run.  Beside it, module_forward_cfg1_cpu times the product's own
+    CPU path (the whole module step)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import torch_reference as TR
+    w = build_workload(torch, dev, CONFIGS["cfg1"], 1)
+    threads = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        kb, kh, km, vp, vm = w["pools"]
+        npb, n = w["np_list"][0], w["tail_list"][0]
+        idx = w["tables"][0][0, :npb].long()
+        sub = [t[idx].cpu() for t in (kb, kh, km, vp, vm)]
+        q, sk, sv, tk, tv, bi = (t.cpu() for t in (w["q"], w["sk"], w["sv"], w["tk"], w["tv"], w["bi"]))
+        times, t_end = [], time.perf_counter() + budget_s
+        while time.perf_counter() < t_end or not times:
+            t0 = time.perf_counter()
+            TR.paged_attention(q[0], range(npb), *sub, bi, w["dk"], sk[0], sv[0], tk[0, :, :n], tv[0, :, :n],
+                               w["Hq"], w["Hkv"], D)
+            times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": round(statistics.median(times) * 1e6, 1), "unit": "us/layer-step", "cores": threads,
+            "kind": "port", **host_cpu(), "runs": len(times),
+            "sample": f"config 1's whole step (1 sequence, {npb} pages, {S} sinks + {n} tail tokens, all "
+                      f"{w['Hkv']} KV heads) through oracle/torch_reference.py, median of {len(times)} runs"}
 
 
 def cpu_baseline_c(w, budget_s: float) -> dict:
@@ -1043,6 +1076,8 @@ def main() -> int:
         result["module_forward_cfg1"] = module_leg(torch, dev, "cfg1")
         log("timing the module on CPU tensors (config 1)")
         result["module_forward_cfg1_cpu"] = module_leg_cpu(torch)
+        if not args.no_cpu_baseline:
+            result["cpu_baseline_cfg1"] = cpu_baseline_cfg1(torch, dev)
     if not args.no_extra:
         log("timing the reference benchmark's items, prefill and the profiler accumulation")
         result["reference_items"] = reference_items(torch, dev)
