@@ -229,11 +229,14 @@ __device__ __forceinline__ void load_rows(const uint16_t *src, int64_t s_tok, in
 }
 
 // Code region of the page (128 rows x 32 B, contiguous): one 16-byte store
-// per thread of the first 256.
+// per thread of the first 256.  The page's outputs are written with the
+// non-temporal hint (they are read back only by later launches): measured
+// 0.3-0.4 us less per config-2 batch than write-back stores.
 __device__ __forceinline__ void store_tile(uint8_t *dst, const unsigned char *tile, int tid)
 {
     if (tid < 256)
-        *(u32x4 *)(dst + 16 * tid) = *(const u32x4 *)(tile + tile_off(tid >> 1) + 16 * (tid & 1));
+        __builtin_nontemporal_store(*(const u32x4 *)(tile + tile_off(tid >> 1) + 16 * (tid & 1)),
+                                    (u32x4 *)(dst + 16 * tid));
 }
 
 // N (4 or 8) consecutive 32-bit LDS words.  (Each element is copied to a
@@ -404,12 +407,12 @@ __device__ void key_block(const QuantLaunch &L, int o, int i, unsigned char *lds
         return;
     store_tile(st.key_low + page * st.key_low_s_page + i * st.key_low_s_head, lds, tid);
     if (tid < 2 * Dk)
-        *(u32x4 *)(st.key_high + page * st.key_high_s_page + i * st.key_high_s_head + 16 * tid) =
-            *(const u32x4 *)(lds + kHighOff + 16 * tid);
+        __builtin_nontemporal_store(*(const u32x4 *)(lds + kHighOff + 16 * tid),
+                                    (u32x4 *)(st.key_high + page * st.key_high_s_page + i * st.key_high_s_head + 16 * tid));
     if (tid < 128) {
         const int64_t m = page * st.key_meta_s_page + i * st.key_meta_s_head + tid;
-        st.key_scale[m] = meta_s;
-        st.key_zero[m] = meta_z;
+        __builtin_nontemporal_store(meta_s, &st.key_scale[m]);
+        __builtin_nontemporal_store(meta_z, &st.key_zero[m]);
     }
 }
 
@@ -466,7 +469,8 @@ __device__ void value_block(const QuantLaunch &L, int o, int i, unsigned char *l
         pz[t] = z;
         const int64_t m = page * st.value_meta_s_page + i * st.value_meta_s_head + 2 * t;
         if (ok)
-            *(unsigned *)(st.value_scale + m) = (unsigned)f2h(s) | ((unsigned)f2h(z) << 16);  // :90, interleaved
+            __builtin_nontemporal_store((unsigned)f2h(s) | ((unsigned)f2h(z) << 16),
+                                        (unsigned *)(st.value_scale + m));  // :90, interleaved
     }
     __syncthreads();
 
