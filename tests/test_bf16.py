@@ -73,7 +73,7 @@ def test_bf16_known_answer_and_double_rounding():
     # the pool holds bf16(fp16(s)), not bf16(s): a boosted channel spanning
     # [-0.5546875, 3.7103891e-06] has s = rng / 15 whose fp16 rounding lands on
     # a bf16 tie (0x3D18 after both roundings, 0x3D17 rounded once)
-    hi = float(O.bf16_to_f32(O.f32_to_bf16(np.float32(3.7103891372680664e-06))))
+    hi = float(O.bf16_to_f32(O.f32_to_bf16(np.float32(3.7103891372680664e-06)))[0])
     row = np.array([[-0.5546875, hi, 0.0, 0.0]], np.float32)
     _, _, s1, _ = O.quantize_key_bf16(O.f32_to_bf16(row), np.zeros(1, np.uint8), 1, 2)
     s_direct = O.f32_to_bf16(np.float32(np.float32(hi) - np.float32(-0.5546875)) / np.float32(15.0))
