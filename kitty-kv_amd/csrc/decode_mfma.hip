@@ -226,24 +226,42 @@ __device__ __forceinline__ void gll16(const unsigned char *src, unsigned char *l
     __builtin_amdgcn_global_load_lds((const void *)src, (__attribute__((address_space(3))) void *)lds_base, 16, 0,
                                      kLoadAux);
 }
+// The same with an immediate offset, which the instruction adds to the
+// global and the LDS address alike.
+template <int OFF>
+__device__ __forceinline__ void gll16_at(const unsigned char *src, unsigned char *lds_base)
+{
+    __builtin_amdgcn_global_load_lds((const void *)src, (__attribute__((address_space(3))) void *)lds_base, 16, OFF,
+                                     kLoadAux);
+}
 
 // Ten direct-to-LDS loads of one (page, head) record; lane l fetches the
 // chunk that belongs in LDS slot l (chunk_global_offset), which applies the
-// bank swizzle without extra instructions.  Lanes past 2*Dk re-read a valid
-// metadata chunk into unused K-high slots, so every page issues exactly
-// kLoadsPerPage loads.
+// bank swizzle without extra instructions.  Lanes past 2*Dk re-read the
+// first K-high chunk (the first key-metadata chunk when Dk = 0) into unused
+// K-high slots, so every page issues exactly kLoadsPerPage loads.  Slot
+// 64 j + l of a 4 KB region is chunk_global_offset(l) + 1024 j, so nine of
+// the loads are a wave-uniform base plus one 32-bit lane offset plus a
+// constant: the SGPR-base form, with no 64-bit address arithmetic per lane.
 constexpr int kLoadsPerPage = 10;
 
 __device__ __forceinline__ void issue_page(unsigned char *st, const PageSrc &s, int lane, int Dk)
 {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int off = chunk_global_offset(64 * j + lane);
-        gll16(s.klo + off, st + kKlo + 1024 * j);
-        gll16(s.val + off, st + kVal + 1024 * j);
-    }
-    gll16(lane < 2 * Dk ? s.khi + chunk_global_offset(lane) : s.kmeta, st + kKhi);
-    gll16(lane < 32 ? s.kmeta + 16 * lane : s.vmeta + 16 * (lane - 32), st + kMeta);
+    uint32_t off = (uint32_t)chunk_global_offset(lane), hoff = lane < 2 * Dk ? off : 0u;
+    // Fresh 32-bit values in the caller's block: a page loop would otherwise
+    // hoist their 64-bit extensions, and the loads would fall back to 64-bit
+    // per-lane addresses.
+    asm volatile("" : "+v"(off), "+v"(hoff));
+    gll16_at<0>(s.klo + off, st + kKlo);
+    gll16_at<0>(s.val + off, st + kVal);
+    gll16_at<1024>(s.klo + off, st + kKlo);
+    gll16_at<1024>(s.val + off, st + kVal);
+    gll16_at<2048>(s.klo + off, st + kKlo);
+    gll16_at<2048>(s.val + off, st + kVal);
+    gll16_at<3072>(s.klo + off, st + kKlo);
+    gll16_at<3072>(s.val + off, st + kVal);
+    gll16((Dk > 0 ? s.khi : s.kmeta) + hoff, st + kKhi);
+    gll16((lane < 32 ? s.kmeta : s.vmeta) + 16u * (uint32_t)(lane & 31), st + kMeta);
 }
 
 template <int N>
