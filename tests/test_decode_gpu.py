@@ -45,6 +45,8 @@ def _to(dev, *arrs):
     (2, 40, 128, 128, 16, 4, 32, 9),  # groups of 20: sub-groups of 16 and 4
     (1, 24, 64, 32, 8, 5, 3, 9),      # generic kernel, a group of 24: 16 and 8
     (2, 16, 128, 128, 32, 3, 7, 0),
+    (2, 8, 128, 128, 5, 4, 32, 60),   # boosted channels not a multiple of 8 (part of a K-high row pair unused)
+    (2, 16, 128, 128, 24, 3, 32, 30), # 24 boosted channels at GQA 8
     (2, 4, 64, 32, 8, 6, 1, 31),
     (2, 4, 256, 128, 32, 2, 5, 17),   # generic kernel at the largest head_dim
     (1, 2, 128, 256, 16, 2, 3, 100),  # and the largest page
