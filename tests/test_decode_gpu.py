@@ -213,6 +213,21 @@ def test_full_size_configs(dev, name, B, Hq, H, ctx, dk):
         _close(out[b], _oracle_batched(c, Hq, H, D, b), f"{name} b={b}")
 
 
+def test_repeated_launches_are_bit_identical(dev):
+    """The split kernel, the merge and the plan use no atomics and no
+    run-time work claiming, so a decode gives the same bits on every launch,
+    also when other decodes (another plan and shape, GQA 8) run in between.
+    Checked for the GQA-4 and GQA-8 kernels on ragged batches."""
+    cases = [_batched_case(dev, 91, 5, 32, 8, 128, 128, 16, [32 + 37 * 128 + 5, 32 + 11 * 128 + 90, 32 + 60 * 128,
+                                                            32 + 2 * 128 + 17, 32 + 25 * 128 + 127]),
+             _batched_case(dev, 92, 3, 16, 2, 128, 128, 32, [32 + 50 * 128 + 64, 32 + 9 * 128 + 3, 32 + 70 * 128 + 1])]
+    first = [_run_batched(dev, c) for c in cases]
+    for _ in range(3):
+        for c, ref in zip(cases, first):
+            out = _run_batched(dev, c)
+            assert np.array_equal(out.view(np.uint16), ref.view(np.uint16))
+
+
 def test_duplicate_boost_ranks_take_the_generic_path(dev):
     """Channels sharing a boost rank read the same high-bit row back
     (dequantize_key.py:70-87) and a channel ranked D_boost has none: the MFMA
