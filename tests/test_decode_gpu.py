@@ -228,6 +228,44 @@ def test_repeated_launches_are_bit_identical(dev):
             assert np.array_equal(out.view(np.uint16), ref.view(np.uint16))
 
 
+def _random_shape(rnd):
+    """One seeded decode shape: the MFMA kernel (D = G = 128, any boosted
+    channel count up to 32) or the generic one, any GQA group up to 32, up
+    to 160 pages, batches past 64 sequences, sink counts 0-32, split sizes."""
+    if rnd.random() < 0.7:
+        D = G = 128
+        dk = rnd.choice([0, 1, 5, 8, 16, 17, 24, 31, 32])
+        maxp = rnd.choice([1, 3, 8, 20, 40, 90, 160])
+    else:
+        D, G = rnd.choice([16, 32, 64, 128, 256]), rnd.choice([8, 16, 32, 64, 128, 256])
+        dk = rnd.choice([0, 1, min(4, D), min(D // 8, 32), min(D // 4, 32)])
+        maxp = rnd.choice([1, 2, 5, 9])
+    H = rnd.choice([1, 2, 4, 8])
+    Hq = H * rnd.choice([1, 2, 3, 4, 5, 6, 8, 12, 16, 20, 24, 32])
+    B = rnd.choice([1, 2, 3, 5, 9, 17]) if rnd.random() < 0.9 else rnd.choice([65, 70])
+    if B > 20:
+        maxp = min(maxp, 3)
+    if maxp > 40:
+        B = min(B, 3)
+    S = rnd.choice([0, 1, 7, 32])
+    ctx = [S + rnd.randint(0, maxp * G + G - 1) for _ in range(B)]
+    return D, G, dk, H, Hq, B, S, ctx, rnd.choice([0, 0, 0, 1, 3, 7, 64])
+
+
+def test_random_shapes_match_oracle(dev):
+    """120 seeded random shapes through the batched decode against the
+    oracle (up to six sequences of each checked)."""
+    import random
+    for k in range(120):
+        rnd = random.Random(7000 + k)
+        D, G, dk, H, Hq, B, S, ctx, pps = _random_shape(rnd)
+        what = f"seed {7000 + k}: D{D} G{G} dk{dk} H{H} Hq{Hq} B{B} S{S} pages_per_split {pps}"
+        c = _batched_case(dev, 7000 + k, B, Hq, H, D, G, dk, ctx, S=S)
+        out = _run_batched(dev, c, pages_per_split=pps)
+        for b in (range(B) if B <= 6 else rnd.sample(range(B), 6)):
+            _close(out[b], _oracle_batched(c, Hq, H, D, b), what + f" b={b}")
+
+
 def test_duplicate_boost_ranks_take_the_generic_path(dev):
     """Channels sharing a boost rank read the same high-bit row back
     (dequantize_key.py:70-87) and a channel ranked D_boost has none: the MFMA
