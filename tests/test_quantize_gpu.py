@@ -103,6 +103,57 @@ def test_small_shapes_and_edge_rows(dev, D, G, Dk, H):
                         Dk, sentinel)
 
 
+def _random_blocks(rnd, gen, n, H, G, D):
+    """(n, H, G, D) fp16 blocks from one of several seeded distributions:
+    normal at a random power-of-two scale (fp16 subnormals to ~2^14), a
+    half-integer grid (every element a tie of some scale), heavy tails,
+    outlier channels, constant tokens / channels."""
+    kind = rnd.choice(["normal", "grid", "heavy", "outlier", "flat"])
+    x = torch.randn(n, H, G, D, generator=gen)
+    if kind == "normal":
+        x = x * 2.0 ** rnd.randint(-20, 12)
+    elif kind == "grid":
+        x = torch.round(x * 4) / 2 * 2.0 ** rnd.randint(-6, 6)
+    elif kind == "heavy":
+        x = x / torch.rand(n, H, G, D, generator=gen).clamp(min=1e-3).sqrt()
+    elif kind == "outlier":
+        x[..., torch.randperm(D, generator=gen)[: max(1, D // 8)]] *= 16.0
+    else:
+        x[:, :, rnd.randrange(G)] = 1.25
+        x[..., rnd.randrange(D)] = -3.0
+    return x.clamp(-60000, 60000).half()
+
+
+def test_random_blocks_bit_exact(dev):
+    """40 seeded random batches (shape, boosted channels, value rows and data
+    distribution drawn per case) through the batch kernel: every page
+    bit-exact against the oracle."""
+    import random
+    from kitty.kernels.ops import quantize_into_pools
+    for k in range(40):
+        rnd = random.Random(900 + k)
+        gen = torch.Generator().manual_seed(900 + k)
+        D, G = rnd.choice([(128, 128)] * 5 + [(16, 8), (64, 32), (32, 16), (256, 128), (128, 256)])
+        Dk = rnd.choice([0, 1, 5, 16, 31, 32]) if D >= 32 else rnd.choice([0, 1, 4])
+        H, n = rnd.choice([1, 2, 8]), rnd.choice([1, 3, 9])
+        sentinel = min(Dk + 1, 255)
+        rows = rnd.choice([None, None, 0, 1, G // 2, G - 1])
+        K = _random_blocks(rnd, gen, n, H, G, D)
+        V = _random_blocks(rnd, gen, n, H, G, D)
+        bi = torch.full((n, H, D), sentinel, dtype=torch.uint8)
+        for o in range(n):
+            for h in range(H):
+                bi[o, h, torch.randperm(D, generator=gen)[:Dk]] = torch.arange(Dk, dtype=torch.uint8)
+        pools, store = _pools(n + 2, H, D, G, Dk, dev)
+        page_ids = torch.randperm(n + 2, generator=gen)[:n].to(torch.int32)
+        quantize_into_pools(store, K.to(dev), V.to(dev), bi.to(dev), page_ids.to(dev), sentinel, value_rows=rows)
+        torch.cuda.synchronize()
+        for o in range(n):
+            for h in range(H):
+                _check_page(pools, int(page_ids[o]), h, K[o, h].numpy().T.copy(), V[o, h].numpy(),
+                            bi[o, h].numpy(), Dk, sentinel, value_rows=rows)
+
+
 def test_duplicate_and_rowless_boost_ranks(dev):
     """Channels sharing a boost rank OR their high bits into the rank's row,
     and a channel ranked D_boost (below the sentinel) gets INT4 codes with no
