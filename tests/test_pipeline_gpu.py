@@ -198,6 +198,63 @@ def test_batched_module_decode_gqa(dev):
                 _close(out[i, :, 0].cpu().numpy(), ref)
 
 
+def test_random_module_sessions(dev):
+    """Seeded random sessions through KittyPagedAttention: per case a shape
+    (head_dim, G, sinks, value window R, KV heads, GQA group), sequences that
+    start with a prefill chunk or with single tokens, then decode steps over
+    random subsets of the unfinished sequences (spills of keys and of the
+    value window at their own times); at random steps every sequence of the
+    step is checked against the oracle rebuilt from its raw token history."""
+    import random
+    from kitty import KittyAttentionFactory
+    shapes = [(16, 8, 4, 8, 60), (16, 8, 4, 5, 60), (16, 8, 0, 0, 50), (32, 16, 3, 16, 90),
+              (128, 128, 32, 128, 420), (128, 128, 32, 128, 300)]
+    for case, (D, G, S, R, maxlen) in enumerate(shapes):
+        rnd = random.Random(400 + case)
+        gen = torch.Generator().manual_seed(400 + case)
+        H = rnd.choice([1, 2]) if D == 128 else rnd.choice([1, 2, 4])
+        Hq = H * rnd.choice([1, 2, 4, 8])
+        B = rnd.choice([2, 3, 4])
+        cfg = _cfg(num_kv_heads=H, head_dim=D, q_buffer_size=G, sink_size=S, local_value_window=R,
+                   boost_rate=0.125 if D == 128 else 0.25, max_seq_len=maxlen + 8, max_batch_size=B)
+        bi = torch.full((1, H, D), cfg.sentinel, dtype=torch.uint8)
+        for h in range(H):
+            bi[0, h, torch.randperm(D, generator=gen)[:cfg.d_boost]] = torch.arange(cfg.d_boost, dtype=torch.uint8)
+        layout, pipe, layers = KittyAttentionFactory.from_config(cfg, bi, Hq)
+        attn = layers[0]
+        lens = [rnd.randint(2, maxlen) for _ in range(B)]
+        hist = [[] for _ in range(B)]
+        # a prefill chunk of one length for a random subset of the sequences
+        pre = [s for s in range(B) if rnd.random() < 0.5]
+        if pre:
+            T = rnd.randint(1, min(lens[s] for s in pre) - 1)
+            k = torch.randn(len(pre), H, T, D, generator=gen).half()
+            v = torch.randn(len(pre), H, T, D, generator=gen).half()
+            q = torch.randn(len(pre), Hq, T, D, generator=gen).half()
+            attn(q.to(dev), k.to(dev), v.to(dev), seq_id=pre)
+            for i, s in enumerate(pre):
+                hist[s].extend((k[i, :, t], v[i, :, t]) for t in range(T))
+        checked = 0
+        while any(len(hist[s]) < lens[s] for s in range(B)):
+            live = [s for s in range(B) if len(hist[s]) < lens[s]]
+            ids = sorted(rnd.sample(live, rnd.randint(1, len(live))))
+            k = torch.randn(len(ids), H, 1, D, generator=gen).half()
+            v = torch.randn(len(ids), H, 1, D, generator=gen).half()
+            q = torch.randn(len(ids), Hq, 1, D, generator=gen).half()
+            out = attn(q.to(dev), k.to(dev), v.to(dev), seq_id=ids)
+            for i, s in enumerate(ids):
+                hist[s].append((k[i, :, 0], v[i, :, 0]))
+            if rnd.random() < 0.08 or all(len(hist[s]) >= lens[s] for s in range(B)):
+                checked += 1
+                for i, s in enumerate(ids):
+                    Kh = torch.stack([a for a, _ in hist[s]]).numpy()
+                    Vh = torch.stack([b for _, b in hist[s]]).numpy()
+                    ref = _oracle_from_history(Kh, Vh, q[i, :, 0].numpy(), S, G, bi[0].numpy(), cfg.d_boost,
+                                               cfg.sentinel, Hq, H, D, R=R)
+                    _close(out[i, :, 0].cpu().numpy(), ref)
+        assert checked > 0
+
+
 def test_prefill_output_is_causal_attention(dev):
     from kitty import KittyAttentionFactory
     cfg = _cfg(num_kv_heads=2, head_dim=16, q_buffer_size=8, sink_size=4)
