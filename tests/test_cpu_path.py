@@ -197,6 +197,25 @@ def test_paged_attention_reference_signature(Hq, H, n_pages, n_sink, n_tail):
             close(out.numpy(), ref)
 
 
+def test_random_decode_shapes_on_cpu():
+    """The GPU suite's seeded random decode shapes (those up to 40 pages and
+    nine sequences) through the CPU path against the oracle."""
+    import random
+    from test_decode_gpu import _batched_case, _oracle_batched, _random_shape, _run_batched
+    cpu_dev, n = torch.device("cpu"), 0
+    for k in range(40):
+        rnd = random.Random(8000 + k)
+        D, G, dk, H, Hq, B, S, ctx, pps = _random_shape(rnd)
+        if max(ctx) > 40 * G or B > 9:
+            continue
+        c = _batched_case(cpu_dev, 8000 + k, B, Hq, H, D, G, dk, ctx, S=S)
+        out = _run_batched(cpu_dev, c, pages_per_split=pps)
+        for b in range(B):
+            close(out[b], _oracle_batched(c, Hq, H, D, b))
+        n += 1
+    assert n >= 20
+
+
 def test_paged_attention_unequal_tails_raise():
     from kitty.kernels import paged_attention
     H, D, G = 2, 16, 8
